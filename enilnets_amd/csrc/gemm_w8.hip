@@ -1,0 +1,509 @@
+// Dense on int8 weights with fp32 activations (the W8 path).
+//
+//   y = act(scale[n] * sum_k x[m,k] * codes[n,k] + bias[n])
+//
+// The codes are integers in [-127, 127], exact in bf16, so the weight side of
+// every MFMA product is exact.  The activations are split into bf16 planes:
+// hi = bf16(x), lo = bf16(x - hi) (ENQ_W8_FP32; residual |x - hi - lo| is
+// about 2^-17 |x|, far inside the 1e-4 * ||row||_inf tolerance), or hi only
+// (ENQ_W8_BF16).  Both planes accumulate into one fp32 MFMA accumulator.
+//
+// Kernels
+//   split_planes_kernel  x (m, k) fp32 -> P bf16 planes (mp, kp), zero padded
+//   gemv_w8_kernel       m <= 64: split-K, W streamed once with 128-bit loads,
+//                        16x16x32 bf16 MFMA, partial sums per K-split
+//   gemv_finish_kernel   sums the K-split partials, scale, bias, activation
+//   w8_gemm_kernel       m > 64: LDS-tiled, double-buffered 32x32x16 bf16
+//                        MFMA GEMM; int8 tiles are expanded to bf16 while
+//                        being staged into LDS; fused epilogue
+#include <algorithm>
+
+#include "common.hpp"
+#include "epilogue.hpp"
+#include "mfma.hpp"
+
+namespace enq {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Activation split into bf16 planes
+// ---------------------------------------------------------------------------
+template <int PLANES>
+__global__ __launch_bounds__(256) void split_planes_kernel(const float* __restrict__ x, int64_t m,
+                                                           int64_t k, uint16_t* __restrict__ out,
+                                                           int64_t mp, int64_t kp, int vec) {
+  // one thread per 8 consecutive elements of a padded row
+  const int64_t groups_per_row = kp / 8;
+  const int64_t gid = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (gid >= mp * groups_per_row) return;
+  const int64_t row = gid / groups_per_row;
+  const int64_t k0 = (gid - row * groups_per_row) * 8;
+  float v[8];
+  if (row < m && vec && k0 + 8 <= k) {
+    const float4 a = *reinterpret_cast<const float4*>(x + row * k + k0);
+    const float4 b = *reinterpret_cast<const float4*>(x + row * k + k0 + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (row < m && k0 + e < k) ? x[row * k + k0 + e] : 0.0f;
+  }
+  Pack8 hi, lo;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    uint16_t h = bf16_bits_rne(v[e]);
+    hi.h[e] = h;
+    if (PLANES == 2) lo.h[e] = bf16_bits_rne(v[e] - bf16_to_float(h));
+  }
+  *reinterpret_cast<Pack8*>(out + row * kp + k0) = hi;
+  if (PLANES == 2) *reinterpret_cast<Pack8*>(out + mp * kp + row * kp + k0) = lo;
+}
+
+// ---------------------------------------------------------------------------
+// Weight loads: 16 int8 codes of row `row` starting at column k0.
+// KMODE 0: k % 32 == 0, aligned rows, no guard.  1: k % 16 == 0, a 16-byte
+// chunk is entirely inside or outside.  2: byte-wise guard.
+// ---------------------------------------------------------------------------
+template <int KMODE>
+__device__ __forceinline__ int4 load_codes16(const int8_t* __restrict__ w, int64_t ldw, int64_t row,
+                                             int64_t k0, int64_t k) {
+  const int8_t* p = w + row * ldw + k0;
+  if constexpr (KMODE == 0) {
+    return *reinterpret_cast<const int4*>(p);
+  } else if constexpr (KMODE == 1) {
+    if (k0 < k) return *reinterpret_cast<const int4*>(p);
+    return make_int4(0, 0, 0, 0);
+  } else {
+    uint32_t wd[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (k0 + e < k) wd[e / 4] |= uint32_t(uint8_t(p[e])) << (8 * (e % 4));
+    return make_int4(int(wd[0]), int(wd[1]), int(wd[2]), int(wd[3]));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV (m <= 64): grid (column groups, K splits), 8 waves per block.  Each
+// wave owns a K range of `chunks` x 128 and keeps the activation fragments of
+// that range in registers; it then streams 16-column blocks of W, and the 8
+// waves' partial tiles are summed through LDS.
+// Lane layout per 128-wide K chunk: lane l covers column n = l % 16 and
+// k = 32 * (l / 16) + [0, 32); MFMA i of the chunk uses k offsets 8i..8i+7.
+// ---------------------------------------------------------------------------
+constexpr int kGemvWaves = 8;
+constexpr int kGemvChunk = 128;
+
+template <int MB, int PLANES, int CHUNKS, int KMODE>
+__global__ __launch_bounds__(512) void gemv_w8_kernel(
+    const uint16_t* __restrict__ xa, int64_t plane_stride, int64_t kp,
+    const int8_t* __restrict__ w, int64_t ldw, int64_t n, int64_t k, int chunks_per_wave,
+    int col_blocks_per_group, float* __restrict__ part) {
+  __shared__ float red[kGemvWaves][MB * 16][17];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int64_t k_wave0 = (int64_t(blockIdx.y) * kGemvWaves + wave) * chunks_per_wave * kGemvChunk;
+
+  // activation fragments for this wave's K range
+  bf16x8 xf[CHUNKS][MB][PLANES][4];
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int64_t kc = k_wave0 + int64_t(c) * kGemvChunk + 32 * grp;
+    const bool live = c < chunks_per_wave && kc < kp;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int p = 0; p < PLANES; ++p) {
+        const uint16_t* src = xa + p * plane_stride + int64_t(mb * 16 + col) * kp + kc;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          xf[c][mb][p][i] = live ? *reinterpret_cast<const bf16x8*>(src + 8 * i) : bf16x8{};
+      }
+  }
+
+  const int64_t mp = MB * 16;
+  for (int cb = 0; cb < col_blocks_per_group; ++cb) {
+    const int64_t n0 = (int64_t(blockIdx.x) * col_blocks_per_group + cb) * 16;
+    if (n0 >= n) break;
+    const int64_t row = n0 + col < n ? n0 + col : n - 1;
+    int4 wc[CHUNKS][2];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int64_t kc = k_wave0 + int64_t(c) * kGemvChunk + 32 * grp;
+      if (c < chunks_per_wave && kc < k) {
+        wc[c][0] = load_codes16<KMODE>(w, ldw, row, kc, k);
+        wc[c][1] = load_codes16<KMODE>(w, ldw, row, kc + 16, k);
+      } else {
+        wc[c][0] = make_int4(0, 0, 0, 0);
+        wc[c][1] = make_int4(0, 0, 0, 0);
+      }
+    }
+    floatx4 acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      bf16x8 wb[4];
+      codes16_to_bf16(wc[c][0], wb[0], wb[1]);
+      codes16_to_bf16(wc[c][1], wb[2], wb[3]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int p = 0; p < PLANES; ++p)
+            acc[mb] = mfma_16x16x32_bf16(xf[c][mb][p][i], wb[i], acc[mb]);
+    }
+    // 16x16 output layout: lane holds column l % 16, rows 4 * (l / 16) + r
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][mb * 16 + 4 * grp + r][col] = acc[mb][r];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < MB * 256; idx += 512) {
+      const int mm = idx >> 4, nn = idx & 15;
+      float s = 0.f;
+#pragma unroll
+      for (int v = 0; v < kGemvWaves; ++v) s += red[v][mm][nn];
+      if (n0 + nn < n) part[(int64_t(blockIdx.y) * mp + mm) * n + n0 + nn] = s;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(256) void gemv_finish_kernel(const float* __restrict__ part,
+                                                          int splits, int64_t mp, int64_t m,
+                                                          int64_t n, const float* __restrict__ scale,
+                                                          const float* __restrict__ bias,
+                                                          Epilogue ep, float* __restrict__ y,
+                                                          float* __restrict__ z) {
+  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= m * n) return;
+  const int64_t row = idx / n, c = idx - row * n;
+  float s = 0.f;
+  for (int sp = 0; sp < splits; ++sp) s += part[(int64_t(sp) * mp + row) * n + c];
+  float v = s * scale[c];
+  if (bias) v = v + bias[c];
+  if (z) z[idx] = v;
+  y[idx] = activate(v, ep);
+}
+
+// ---------------------------------------------------------------------------
+// GEMM (m > 64): BM x BN block tile, BK = 32, WM x WN waves.
+// LDS rows are 32 bf16 + 8 pad (80 bytes): 16 consecutive rows then fall in
+// 16 distinct 16-byte bank groups for the MFMA operand reads.
+// ---------------------------------------------------------------------------
+constexpr int kBK = 32;
+constexpr int kPitch = 40;  // bf16 elements per LDS row
+
+template <int BM, int BN, int WM, int WN, int PLANES, int KMODE>
+__global__ __launch_bounds__(WM * WN * 64) void w8_gemm_kernel(
+    const uint16_t* __restrict__ xa, int64_t plane_stride, int64_t kp,
+    const int8_t* __restrict__ w, int64_t ldw, const float* __restrict__ scale,
+    const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_n,
+    Epilogue ep, float* __restrict__ y, float* __restrict__ z) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int A_CHUNKS = PLANES * BM * (kBK / 8);  // 16-byte chunks per stage
+  constexpr int B_CHUNKS = BN * (kBK / 16);          // 16 codes per chunk
+  static_assert(A_CHUNKS % NT == 0, "A tile must split evenly over threads");
+  static_assert(B_CHUNKS <= NT && NT % B_CHUNKS == 0, "B tile must split over threads");
+  constexpr int A_PER_T = A_CHUNKS / NT;
+
+  extern __shared__ __align__(16) uint16_t lds[];
+  uint16_t* lds_a = lds;                                  // [2][PLANES][BM][kPitch]
+  uint16_t* lds_b = lds + 2 * PLANES * BM * kPitch;       // [2][BN][kPitch]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int tile = blockIdx.x;
+  const int64_t m0 = int64_t(tile / tiles_n) * BM;
+  const int64_t n0 = int64_t(tile % tiles_n) * BN;
+
+  // global -> register staging
+  int4 a_reg[A_PER_T];
+  int4 b_reg;
+  const bool b_loader = tid < B_CHUNKS;
+
+  auto load_stage = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int q = tid + i * NT;
+      const int p = q / (BM * 4);
+      const int r = (q / 4) % BM;
+      const int c = q % 4;
+      int64_t row = m0 + r;
+      row = row < m ? row : m - 1;
+      a_reg[i] = *reinterpret_cast<const int4*>(xa + p * plane_stride + row * kp + k0 + c * 8);
+    }
+    if (b_loader) {
+      const int r = tid / 2, h = tid % 2;
+      int64_t row = n0 + r;
+      row = row < n ? row : n - 1;
+      b_reg = load_codes16<KMODE>(w, ldw, row, k0 + h * 16, k);
+    }
+  };
+  auto store_stage = [&](int buf) {
+    uint16_t* la = lds_a + buf * PLANES * BM * kPitch;
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int q = tid + i * NT;
+      const int p = q / (BM * 4);
+      const int r = (q / 4) % BM;
+      const int c = q % 4;
+      *reinterpret_cast<int4*>(la + (p * BM + r) * kPitch + c * 8) = a_reg[i];
+    }
+    if (b_loader) {
+      const int r = tid / 2, h = tid % 2;
+      bf16x8 lo8, hi8;
+      codes16_to_bf16(b_reg, lo8, hi8);
+      uint16_t* lb = lds_b + buf * BN * kPitch + r * kPitch + h * 16;
+      *reinterpret_cast<bf16x8*>(lb) = lo8;
+      *reinterpret_cast<bf16x8*>(lb + 8) = hi8;
+    }
+  };
+
+  floatx16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int ktiles = int(kp / kBK);
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  if (ktiles > 1) load_stage(kBK);
+
+  const int lrow = lane & 31;
+  const int lk = (lane >> 5) * 8;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int buf = kt & 1;
+    const uint16_t* la = lds_a + buf * PLANES * BM * kPitch;
+    const uint16_t* lb = lds_b + buf * BN * kPitch;
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      bf16x8 af[FM][PLANES], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int p = 0; p < PLANES; ++p)
+          af[i][p] = *reinterpret_cast<const bf16x8*>(
+              la + (p * BM + wm * TM + i * 32 + lrow) * kPitch + ks * 16 + lk);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(lb + (wn * TN + j * 32 + lrow) * kPitch +
+                                                  ks * 16 + lk);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int p = 0; p < PLANES; ++p)
+            acc[i][j] = mfma_32x32x16_bf16(af[i][p], bfr[j], acc[i][j]);
+    }
+    if (kt + 1 < ktiles) {
+      store_stage(buf ^ 1);
+      if (kt + 2 < ktiles) load_stage(int64_t(kt + 2) * kBK);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds column l % 32, rows 8 * (e / 4) + 4 * (l / 32) + e % 4
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t col = n0 + wn * TN + j * 32 + (lane & 31);
+    if (col >= n) continue;
+    const float s = scale[col];
+    const float b = bias ? bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+        if (row < m) {
+          float v = acc[i][j][e] * s;
+          if (bias) v = v + b;
+          if (z) z[row * n + col] = v;
+          y[row * n + col] = activate(v, ep);
+        }
+      }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int PLANES, int KMODE>
+void launch_gemm(const uint16_t* xa, int64_t plane_stride, int64_t kp, const int8_t* w,
+                 int64_t ldw, const float* scale, const float* bias, int64_t m, int64_t n,
+                 int64_t k, const Epilogue& ep, float* y, float* z) {
+  const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
+  ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
+  const size_t lds_bytes = size_t(2) * (PLANES * BM + BN) * kPitch * sizeof(uint16_t);
+  auto kernel = w8_gemm_kernel<BM, BN, WM, WN, PLANES, KMODE>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
+    attr_set = true;
+  }
+  kernel<<<unsigned(tiles_m * tiles_n), WM * WN * 64, lds_bytes, stream()>>>(
+      xa, plane_stride, kp, w, ldw, scale, bias, m, n, k, int(tiles_n), ep, y, z);
+  check_launch("w8_gemm_kernel");
+}
+
+template <int PLANES, int KMODE>
+void gemm_dispatch(const uint16_t* xa, int64_t plane_stride, int64_t kp, const int8_t* w,
+                   int64_t ldw, const float* scale, const float* bias, int64_t m, int64_t n,
+                   int64_t k, const Epilogue& ep, float* y, float* z) {
+  const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256);
+  if (big_tiles >= device_cu_count())
+    launch_gemm<256, 256, 4, 2, PLANES, KMODE>(xa, plane_stride, kp, w, ldw, scale, bias, m, n, k,
+                                               ep, y, z);
+  else
+    launch_gemm<128, 128, 2, 2, PLANES, KMODE>(xa, plane_stride, kp, w, ldw, scale, bias, m, n, k,
+                                               ep, y, z);
+}
+
+// Launch geometry of the GEMV: K splits, K chunks per wave, 16-column blocks
+// per block group.
+struct GemvPlan {
+  int mb;      // 16-row activation blocks (1, 2 or 4)
+  int chunks;  // template bound on K chunks per wave
+  int64_t splits;
+  int chunks_per_wave;
+  int cb_per_group;
+  int64_t groups;
+};
+
+GemvPlan plan_gemv(int64_t m, int64_t n, int64_t kp) {
+  GemvPlan g;
+  g.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  g.chunks = m <= 16 ? 2 : 1;
+  const int64_t chunks_total = ceil_div(kp, kGemvChunk);
+  g.splits = ceil_div(chunks_total, int64_t(kGemvWaves) * g.chunks);
+  g.chunks_per_wave = int(ceil_div(chunks_total, g.splits * kGemvWaves));
+  const int64_t col_blocks = ceil_div(n, 16);
+  // enough column groups to fill the device together with the K splits
+  const int64_t want_groups = std::max<int64_t>(1, (int64_t(device_cu_count()) * 2) / g.splits);
+  int cb = int(std::max<int64_t>(1, col_blocks / want_groups));
+  g.cb_per_group = std::min(cb, 8);
+  g.groups = ceil_div(col_blocks, g.cb_per_group);
+  ENQ_REQUIRE(g.groups <= 0x7fffffff && g.splits <= 65535, "problem too large");
+  return g;
+}
+
+template <int MB, int PLANES, int CHUNKS, int KMODE>
+void launch_gemv(const GemvPlan& g, const uint16_t* xa, int64_t plane_stride, int64_t kp,
+                 const int8_t* w, int64_t ldw, const float* scale, const float* bias, int64_t m,
+                 int64_t n, int64_t k, const Epilogue& ep, float* y, float* z, float* part) {
+  const int64_t mp = MB * 16;
+  gemv_w8_kernel<MB, PLANES, CHUNKS, KMODE>
+      <<<dim3(unsigned(g.groups), unsigned(g.splits)), 512, 0, stream()>>>(
+          xa, plane_stride, kp, w, ldw, n, k, g.chunks_per_wave, g.cb_per_group, part);
+  check_launch("gemv_w8_kernel");
+  const int64_t total = m * n;
+  gemv_finish_kernel<<<unsigned(ceil_div(total, 256)), 256, 0, stream()>>>(
+      part, int(g.splits), mp, m, n, scale, bias, ep, y, z);
+  check_launch("gemv_finish_kernel");
+}
+
+template <int PLANES, int KMODE>
+void gemv_dispatch(const GemvPlan& g, const uint16_t* xa, int64_t plane_stride, int64_t kp,
+                   const int8_t* w, int64_t ldw, const float* scale, const float* bias, int64_t m,
+                   int64_t n, int64_t k, const Epilogue& ep, float* y, float* z, float* part) {
+  if (g.mb == 1)
+    launch_gemv<1, PLANES, 2, KMODE>(g, xa, plane_stride, kp, w, ldw, scale, bias, m, n, k, ep,
+                                     y, z, part);
+  else if (g.mb == 2)
+    launch_gemv<2, PLANES, 1, KMODE>(g, xa, plane_stride, kp, w, ldw, scale, bias, m, n, k, ep,
+                                     y, z, part);
+  else
+    launch_gemv<4, PLANES, 1, KMODE>(g, xa, plane_stride, kp, w, ldw, scale, bias, m, n, k, ep,
+                                     y, z, part);
+}
+
+}  // namespace
+
+void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const float* w_scale,
+              int64_t n, const float* bias, const Epilogue& ep, int variant, float* y, float* z) {
+  const int planes = variant == ENQ_W8_FP32 ? 2 : 1;
+  const bool gemv = m <= 64;
+  const int64_t kp = ceil_div(k, gemv ? kGemvChunk : kBK) * (gemv ? kGemvChunk : kBK);
+  const int64_t mp = gemv ? (m <= 16 ? 16 : (m <= 32 ? 32 : 64)) : m;
+  const int64_t plane_stride = mp * kp;
+  const size_t planes_bytes = ((size_t(planes) * plane_stride * sizeof(uint16_t)) + 255) / 256 * 256;
+  GemvPlan plan{};
+  size_t part_bytes = 0;
+  if (gemv) {
+    plan = plan_gemv(m, n, kp);
+    part_bytes = sizeof(float) * size_t(plan.splits) * size_t(mp) * size_t(n);
+  }
+  // one allocation for everything this call needs, taken before any launch
+  char* ws = static_cast<char*>(workspace(planes_bytes + part_bytes));
+  auto* xa = reinterpret_cast<uint16_t*>(ws);
+  float* part = reinterpret_cast<float*>(ws + planes_bytes);
+  {
+    const int64_t groups = mp * (kp / 8);
+    const int vec = (k % 4 == 0) && aligned(x, 16);
+    if (planes == 2)
+      split_planes_kernel<2><<<unsigned(ceil_div(groups, 256)), 256, 0, stream()>>>(x, m, k, xa,
+                                                                                    mp, kp, vec);
+    else
+      split_planes_kernel<1><<<unsigned(ceil_div(groups, 256)), 256, 0, stream()>>>(x, m, k, xa,
+                                                                                    mp, kp, vec);
+    check_launch("split_planes_kernel");
+  }
+  const int kmode = (k % 32 == 0 && aligned(codes, 16)) ? 0 : ((k % 16 == 0 && aligned(codes, 16)) ? 1 : 2);
+  // the K-split GEMV pads K to 128 and needs chunk guards unless k is a multiple of 128
+  const int gemv_kmode = kmode == 0 ? (k % 128 == 0 ? 0 : 1) : kmode;
+  auto run = [&](auto planes_tag, auto kmode_tag) {
+    constexpr int P = decltype(planes_tag)::value;
+    constexpr int KM = decltype(kmode_tag)::value;
+    if (gemv)
+      gemv_dispatch<P, KM>(plan, xa, plane_stride, kp, codes, k, w_scale, bias, m, n, k, ep, y, z,
+                           part);
+    else
+      gemm_dispatch<P, KM>(xa, plane_stride, kp, codes, k, w_scale, bias, m, n, k, ep, y, z);
+  };
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2>;
+  using K0 = std::integral_constant<int, 0>;
+  using K1 = std::integral_constant<int, 1>;
+  using K2 = std::integral_constant<int, 2>;
+  const int km = gemv ? gemv_kmode : kmode;
+  if (planes == 2) {
+    if (km == 0) run(P2{}, K0{});
+    else if (km == 1) run(P2{}, K1{});
+    else run(P2{}, K2{});
+  } else {
+    if (km == 0) run(P1{}, K0{});
+    else if (km == 1) run(P1{}, K1{});
+    else run(P1{}, K2{});
+  }
+  if (ep.activation == ENQ_ACT_SOFTMAX) softmax_rows(y, m, n);
+}
+
+}  // namespace enq
+
+using namespace enq;
+
+extern "C" int enq_dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes,
+                            const float* w_scale, int64_t n, const float* bias, int activation,
+                            float act_alpha, float act_clip, int variant, float* y, float* z) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && n >= 1 && k >= 1, "m, n, k must be positive (m=%lld n=%lld k=%lld)",
+                (long long)m, (long long)n, (long long)k);
+    ENQ_REQUIRE(x && codes && w_scale && y, "NULL pointer argument");
+    ENQ_REQUIRE(valid_activation(activation), "unknown activation code %d", activation);
+    ENQ_REQUIRE(variant == ENQ_W8_FP32 || variant == ENQ_W8_BF16, "unknown variant %d", variant);
+    Epilogue ep{activation, act_alpha, act_clip};
+    dense_w8(x, m, k, codes, w_scale, n, bias, ep, variant, y, z);
+  });
+}

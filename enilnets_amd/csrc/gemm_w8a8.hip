@@ -1,0 +1,258 @@
+// W8A8 Dense: int8 activation codes x int8 weight codes on the int8 matrix
+// cores, int32 accumulation, fp32 epilogue.
+//
+//   acc[m,n] = sum_k xq[m,k] * wq[n,k]                       (exact int32)
+//   y[m,n]   = act(((float)acc * x_scale[m]) * w_scale[n] + bias[n])
+//
+// The epilogue is evaluated in exactly that order with no fused multiply-add,
+// so for the linear activation y is bit-identical to the NumPy composition
+//   (acc.astype(float32) * x_scale) * w_scale.T + b.
+#pragma clang fp contract(off)
+
+#include "common.hpp"
+#include "epilogue.hpp"
+#include "mfma.hpp"
+
+namespace enq {
+
+void quantize_rows_i8_internal(const float* x, int64_t rows, int64_t cols, int8_t* codes,
+                               float* scale, float* zp_scratch);
+
+namespace {
+
+constexpr int kBK8 = 64;     // int8 codes per row per stage
+constexpr int kPitch8 = 80;  // bytes per LDS row (64 + 16 pad)
+
+// 16 codes of row `row` at column k0 of an (rows, k) int8 matrix.
+template <int KMODE>
+__device__ __forceinline__ int4 load_i8x16(const int8_t* __restrict__ base, int64_t ld,
+                                           int64_t row, int64_t k0, int64_t k) {
+  const int8_t* p = base + row * ld + k0;
+  if constexpr (KMODE == 0) {
+    return *reinterpret_cast<const int4*>(p);
+  } else if constexpr (KMODE == 1) {
+    if (k0 < k) return *reinterpret_cast<const int4*>(p);
+    return make_int4(0, 0, 0, 0);
+  } else {
+    uint32_t wd[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (k0 + e < k) wd[e / 4] |= uint32_t(uint8_t(p[e])) << (8 * (e % 4));
+    return make_int4(int(wd[0]), int(wd[1]), int(wd[2]), int(wd[3]));
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int KMODE>
+__global__ __launch_bounds__(WM * WN * 64) void w8a8_gemm_kernel(
+    const int8_t* __restrict__ xq, const float* __restrict__ x_scale,
+    const int8_t* __restrict__ wq, const float* __restrict__ w_scale,
+    const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_n, Epilogue ep,
+    float* __restrict__ y, int32_t* __restrict__ acc_out) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int A_CHUNKS = BM * (kBK8 / 16);
+  constexpr int B_CHUNKS = BN * (kBK8 / 16);
+  static_assert(A_CHUNKS % NT == 0 && B_CHUNKS % NT == 0, "tiles must split over threads");
+  constexpr int A_PER_T = A_CHUNKS / NT, B_PER_T = B_CHUNKS / NT;
+
+  extern __shared__ __align__(16) int8_t lds8[];
+  int8_t* lds_a = lds8;                         // [2][BM][kPitch8]
+  int8_t* lds_b = lds8 + 2 * BM * kPitch8;      // [2][BN][kPitch8]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int tile = blockIdx.x;
+  const int64_t m0 = int64_t(tile / tiles_n) * BM;
+  const int64_t n0 = int64_t(tile % tiles_n) * BN;
+
+  int4 a_reg[A_PER_T], b_reg[B_PER_T];
+  auto load_stage = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int q = tid + i * NT;
+      const int r = q / 4, c = q % 4;
+      int64_t row = m0 + r;
+      row = row < m ? row : m - 1;
+      a_reg[i] = load_i8x16<KMODE>(xq, k, row, k0 + c * 16, k);
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER_T; ++i) {
+      const int q = tid + i * NT;
+      const int r = q / 4, c = q % 4;
+      int64_t row = n0 + r;
+      row = row < n ? row : n - 1;
+      b_reg[i] = load_i8x16<KMODE>(wq, k, row, k0 + c * 16, k);
+    }
+  };
+  auto store_stage = [&](int buf) {
+    int8_t* la = lds_a + buf * BM * kPitch8;
+    int8_t* lb = lds_b + buf * BN * kPitch8;
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int q = tid + i * NT;
+      *reinterpret_cast<int4*>(la + (q / 4) * kPitch8 + (q % 4) * 16) = a_reg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER_T; ++i) {
+      const int q = tid + i * NT;
+      *reinterpret_cast<int4*>(lb + (q / 4) * kPitch8 + (q % 4) * 16) = b_reg[i];
+    }
+  };
+
+  intx16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+  const int ktiles = int(ceil_div(k, kBK8));
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  if (ktiles > 1) load_stage(kBK8);
+
+  const int lrow = lane & 31;
+  const int lk = (lane >> 5) * 16;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int buf = kt & 1;
+    const int8_t* la = lds_a + buf * BM * kPitch8;
+    const int8_t* lb = lds_b + buf * BN * kPitch8;
+#pragma unroll
+    for (int ks = 0; ks < kBK8 / 32; ++ks) {
+      intx4 af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = *reinterpret_cast<const intx4*>(la + (wm * TM + i * 32 + lrow) * kPitch8 +
+                                                ks * 32 + lk);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = *reinterpret_cast<const intx4*>(lb + (wn * TN + j * 32 + lrow) * kPitch8 +
+                                                 ks * 32 + lk);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma_32x32x32_i8(af[i], bfr[j], acc[i][j]);
+    }
+    if (kt + 1 < ktiles) {
+      store_stage(buf ^ 1);
+      if (kt + 2 < ktiles) load_stage(int64_t(kt + 2) * kBK8);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t col = n0 + wn * TN + j * 32 + (lane & 31);
+    if (col >= n) continue;
+    const float sw = w_scale[col];
+    const float b = bias ? bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+        if (row < m) {
+          const int32_t a = acc[i][j][e];
+          if (acc_out) acc_out[row * n + col] = a;
+          float v = float(a) * x_scale[row];
+          v = v * sw;
+          if (bias) v = v + b;
+          y[row * n + col] = activate(v, ep);
+        }
+      }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int KMODE>
+void launch_w8a8(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws,
+                 const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep, float* y,
+                 int32_t* acc) {
+  const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
+  ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
+  const size_t lds_bytes = size_t(2) * (BM + BN) * kPitch8;
+  auto kernel = w8a8_gemm_kernel<BM, BN, WM, WN, KMODE>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
+    attr_set = true;
+  }
+  kernel<<<unsigned(tiles_m * tiles_n), WM * WN * 64, lds_bytes, stream()>>>(
+      xq, xs, wq, ws, bias, m, n, k, int(tiles_n), ep, y, acc);
+  check_launch("w8a8_gemm_kernel");
+}
+
+template <int KMODE>
+void w8a8_dispatch(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws,
+                   const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep,
+                   float* y, int32_t* acc) {
+  const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256);
+  if (big_tiles >= device_cu_count())
+    launch_w8a8<256, 256, 4, 2, KMODE>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+  else
+    launch_w8a8<128, 128, 2, 2, KMODE>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+}
+
+}  // namespace
+
+void gemm_w8a8(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws,
+               const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep, float* y,
+               int32_t* acc) {
+  const bool al = aligned(xq, 16) && aligned(wq, 16);
+  if (k % kBK8 == 0 && al)
+    w8a8_dispatch<0>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+  else if (k % 16 == 0 && al)
+    w8a8_dispatch<1>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+  else
+    w8a8_dispatch<2>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+  if (ep.activation == ENQ_ACT_SOFTMAX) softmax_rows(y, m, n);
+}
+
+}  // namespace enq
+
+using namespace enq;
+
+extern "C" {
+
+int enq_gemm_w8a8(const int8_t* x_codes, const float* x_scale, const int8_t* w_codes,
+                  const float* w_scale, const float* bias, int64_t m, int64_t n, int64_t k,
+                  int activation, float act_alpha, float act_clip, float* y, int32_t* acc) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && n >= 1 && k >= 1, "m, n, k must be positive");
+    ENQ_REQUIRE(k <= 133143, "k=%lld can overflow the int32 accumulator (max 133143)",
+                (long long)k);
+    ENQ_REQUIRE(x_codes && x_scale && w_codes && w_scale && y, "NULL pointer argument");
+    ENQ_REQUIRE(valid_activation(activation), "unknown activation code %d", activation);
+    Epilogue ep{activation, act_alpha, act_clip};
+    gemm_w8a8(x_codes, x_scale, w_codes, w_scale, bias, m, n, k, ep, y, acc);
+  });
+}
+
+int enq_dense_w8a8(const float* x, int64_t m, int64_t k, const int8_t* codes,
+                   const float* w_scale, int64_t n, const float* bias, int activation,
+                   float act_alpha, float act_clip, float* y, int32_t* acc) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && n >= 1 && k >= 1, "m, n, k must be positive");
+    ENQ_REQUIRE(k <= 133143, "k=%lld can overflow the int32 accumulator (max 133143)",
+                (long long)k);
+    ENQ_REQUIRE(x && codes && w_scale && y, "NULL pointer argument");
+    ENQ_REQUIRE(valid_activation(activation), "unknown activation code %d", activation);
+    const size_t code_bytes = (size_t(m) * size_t(k) + 255) / 256 * 256;
+    char* ws = static_cast<char*>(workspace(code_bytes + 2 * sizeof(float) * size_t(m)));
+    auto* xq = reinterpret_cast<int8_t*>(ws);
+    auto* xs = reinterpret_cast<float*>(ws + code_bytes);
+    float* zp = xs + m;
+    quantize_rows_i8_internal(x, m, k, xq, xs, zp);
+    Epilogue ep{activation, act_alpha, act_clip};
+    gemm_w8a8(xq, xs, codes, w_scale, bias, m, n, k, ep, y, acc);
+  });
+}
+
+}  // extern "C"

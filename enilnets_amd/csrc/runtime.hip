@@ -1,0 +1,259 @@
+// Library lifecycle, errors, device memory, copies and event timing.
+#include <cstdarg>
+#include <cstring>
+#include <mutex>
+
+#include "common.hpp"
+
+namespace enq {
+
+namespace {
+
+thread_local std::string g_error;
+
+struct DeviceState {
+  bool ready = false;
+  int device = -1;
+  int cu_count = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t user_stream = nullptr;  // enq_set_stream
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+};
+
+DeviceState g_state;
+std::mutex g_mutex;
+
+}  // namespace
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+}
+
+const char* last_error() { return g_error.c_str(); }
+
+void fail(int status, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  throw Failure{status};
+}
+
+void require_init() {
+  if (!g_state.ready)
+    fail(ENQ_ERR_NO_DEVICE, "enilnets_amd is not initialised: call enq_init(device) first");
+  int cur = -1;
+  ENQ_HIP(hipGetDevice(&cur));
+  if (cur != g_state.device) ENQ_HIP(hipSetDevice(g_state.device));
+}
+
+hipStream_t stream() {
+  return g_state.user_stream ? g_state.user_stream : g_state.own_stream;
+}
+
+int device_cu_count() { return g_state.cu_count; }
+
+void* workspace(size_t bytes) {
+  std::lock_guard<std::mutex> lock(g_mutex);
+  if (bytes <= g_state.workspace_bytes) return g_state.workspace;
+  // Round up so repeated small growth does not reallocate every call.
+  size_t want = 1u << 20;
+  while (want < bytes) want <<= 1;
+  if (g_state.workspace) {
+    // Earlier work on the stream may still read the old buffer.
+    ENQ_HIP(hipStreamSynchronize(stream()));
+    ENQ_HIP(hipFree(g_state.workspace));
+    g_state.workspace = nullptr;
+    g_state.workspace_bytes = 0;
+  }
+  ENQ_HIP(hipMalloc(&g_state.workspace, want));
+  g_state.workspace_bytes = want;
+  return g_state.workspace;
+}
+
+void check_launch(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    fail(ENQ_ERR_RUNTIME, "launch of %s failed: %s", what, hipGetErrorString(err));
+}
+
+}  // namespace enq
+
+using namespace enq;
+
+extern "C" {
+
+int enq_abi_version(void) { return ENQ_ABI_VERSION; }
+
+const char* enq_last_error(void) { return last_error(); }
+
+int enq_init(int device) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (g_state.ready && g_state.device == device) return;
+    int count = 0;
+    hipError_t err = hipGetDeviceCount(&count);
+    if (err != hipSuccess || count == 0)
+      fail(ENQ_ERR_NO_DEVICE, "no HIP device visible (%s)",
+           err == hipSuccess ? "device count is 0" : hipGetErrorString(err));
+    if (device < 0 || device >= count)
+      fail(ENQ_ERR_INVALID, "device %d out of range [0, %d)", device, count);
+    hipDeviceProp_t prop;
+    ENQ_HIP(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+      fail(ENQ_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 only",
+           device, prop.gcnArchName);
+    if (g_state.ready) {
+      ENQ_HIP(hipStreamSynchronize(g_state.own_stream));
+      ENQ_HIP(hipStreamDestroy(g_state.own_stream));
+      if (g_state.workspace) ENQ_HIP(hipFree(g_state.workspace));
+      g_state = DeviceState{};
+    }
+    ENQ_HIP(hipSetDevice(device));
+    hipStream_t s = nullptr;
+    // Default priority on purpose: streams of mixed priority are avoided.
+    ENQ_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    g_state.device = device;
+    g_state.cu_count = prop.multiProcessorCount;
+    g_state.own_stream = s;
+    g_state.ready = true;
+  });
+}
+
+int enq_get_device_info(enq_device_info* out) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(out != nullptr, "out is NULL");
+    hipDeviceProp_t prop;
+    ENQ_HIP(hipGetDeviceProperties(&prop, g_state.device));
+    std::memset(out, 0, sizeof(*out));
+    std::strncpy(out->name, prop.name, sizeof(out->name) - 1);
+    std::strncpy(out->arch, prop.gcnArchName, sizeof(out->arch) - 1);
+    out->device = g_state.device;
+    out->compute_units = prop.multiProcessorCount;
+    out->clock_khz = prop.clockRate;
+    out->memory_clock_khz = prop.memoryClockRate;
+    out->memory_bus_width = prop.memoryBusWidth;
+    out->l2_bytes = prop.l2CacheSize;
+    out->lds_bytes_per_block = static_cast<int>(prop.sharedMemPerBlock);
+    out->wavefront_size = prop.warpSize;
+    out->global_memory_bytes = static_cast<long long>(prop.totalGlobalMem);
+  });
+}
+
+int enq_synchronize(void) {
+  return guarded([&] {
+    require_init();
+    ENQ_HIP(hipStreamSynchronize(stream()));
+  });
+}
+
+int enq_get_stream(void** s) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(s != nullptr, "stream out-pointer is NULL");
+    *s = stream();
+  });
+}
+
+int enq_set_stream(void* s) {
+  return guarded([&] {
+    require_init();
+    g_state.user_stream = static_cast<hipStream_t>(s);
+  });
+}
+
+int enq_malloc(void** dptr, size_t bytes) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(dptr != nullptr, "dptr is NULL");
+    *dptr = nullptr;
+    if (bytes == 0) return;
+    ENQ_HIP(hipMalloc(dptr, bytes));
+  });
+}
+
+int enq_free(void* dptr) {
+  return guarded([&] {
+    require_init();
+    if (dptr == nullptr) return;
+    // Work already enqueued may still use the buffer.
+    ENQ_HIP(hipStreamSynchronize(stream()));
+    ENQ_HIP(hipFree(dptr));
+  });
+}
+
+int enq_copy_to_device(void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    require_init();
+    if (bytes == 0) return;
+    ENQ_REQUIRE(dst && src, "NULL pointer in copy");
+    ENQ_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream()));
+    ENQ_HIP(hipStreamSynchronize(stream()));
+  });
+}
+
+int enq_copy_to_host(void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    require_init();
+    if (bytes == 0) return;
+    ENQ_REQUIRE(dst && src, "NULL pointer in copy");
+    ENQ_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream()));
+    ENQ_HIP(hipStreamSynchronize(stream()));
+  });
+}
+
+int enq_copy_on_device(void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    require_init();
+    if (bytes == 0) return;
+    ENQ_REQUIRE(dst && src, "NULL pointer in copy");
+    ENQ_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, stream()));
+    ENQ_HIP(hipStreamSynchronize(stream()));
+  });
+}
+
+int enq_event_create(void** event) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(event != nullptr, "event out-pointer is NULL");
+    hipEvent_t e;
+    ENQ_HIP(hipEventCreate(&e));
+    *event = e;
+  });
+}
+
+int enq_event_destroy(void* event) {
+  return guarded([&] {
+    require_init();
+    if (event) ENQ_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)));
+  });
+}
+
+int enq_event_record(void* event) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(event != nullptr, "event is NULL");
+    ENQ_HIP(hipEventRecord(static_cast<hipEvent_t>(event), stream()));
+  });
+}
+
+int enq_event_elapsed_ms(void* start, void* end, float* ms) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(start && end && ms, "NULL argument");
+    ENQ_HIP(hipEventSynchronize(static_cast<hipEvent_t>(end)));
+    ENQ_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
+                                static_cast<hipEvent_t>(end)));
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,120 @@
+"""Dense layers on int8 weights, device-resident.
+
+``dense_w8`` is the fp32-activation path (``Enilnets/nn/forward.py:317-321``
+with the fake-quantized weights); ``dense_w8a8`` the integer path with
+per-token activation codes.  Inputs and outputs are ``DeviceArray``s, so a
+model's layers chain in HBM without host round trips.
+"""
+
+from typing import Any, Dict, Optional, Tuple
+
+import numpy as np
+
+from .. import _lib
+from ..device import DeviceArray, null
+from .weights import Int8Weights
+
+VARIANTS = {"fp32": _lib.W8_FP32, "bf16": _lib.W8_BF16}
+
+#: ``Enilnets/core/constants.py:18,21,22``.
+SIGMOID_CLIP = 500.0
+LEAKYRELU_ALPHA = 0.01
+ELU_ALPHA = 1.0
+
+
+def activation_args(name: str, params: Optional[Dict[str, Any]] = None) -> Tuple[int, float, float]:
+    """(code, alpha, clip) of an activation (``nn/activations.py:6-42``);
+    ValueError for an unknown name, as ``activate`` raises."""
+    if name not in _lib.ACTIVATIONS:
+        raise ValueError(f"Unknown activation: {name!r}")
+    params = params or {}
+    alpha = params.get("alpha")
+    if alpha is None:
+        alpha = ELU_ALPHA if name == "elu" else LEAKYRELU_ALPHA
+    clip = params.get("sigmoid_clip")
+    if clip is None:
+        clip = SIGMOID_CLIP
+    return _lib.ACTIVATIONS[name], float(alpha), float(clip)
+
+
+def _rows(x: DeviceArray) -> Tuple[int, int]:
+    k = x.shape[-1]
+    return x.size // max(k, 1), k
+
+
+def dense_w8(x: DeviceArray, w: Int8Weights, bias: Optional[DeviceArray] = None,
+             activation: str = "linear", activation_params: Optional[Dict[str, Any]] = None,
+             variant: str = "fp32", out: Optional[DeviceArray] = None,
+             pre_activation: Optional[DeviceArray] = None) -> DeviceArray:
+    """``act(x @ (codes * scale).T + bias)`` for fp32 ``x`` of shape
+    ``(..., k)`` and int8 weights ``(n, k)``."""
+    if x.dtype != np.float32:
+        raise NotImplementedError(f"W8 Dense takes float32 activations, got {x.dtype}")
+    m, k = _rows(x)
+    n, wk = w.shape[-2], w.shape[-1]
+    if len(w.shape) != 2:
+        raise ValueError(f"dense weights must be 2-D, got shape {w.shape}")
+    if wk != k:
+        raise ValueError(f"shapes {x.shape} and {w.shape} not aligned: {k} (dim -1) != {wk}")
+    code, alpha, clip = activation_args(activation, activation_params)
+    out_shape = x.shape[:-1] + (n,)
+    y = out if out is not None else DeviceArray(out_shape, np.float32)
+    _lib.call("enq_dense_w8", x.ptr, m, k, w.codes.ptr, w.scale.ptr, n,
+              bias.ptr if bias is not None else null(), code, alpha, clip, VARIANTS[variant],
+              y.ptr, pre_activation.ptr if pre_activation is not None else null())
+    return y
+
+
+def dense_w8a8(x: DeviceArray, w: Int8Weights, bias: Optional[DeviceArray] = None,
+               activation: str = "linear", activation_params: Optional[Dict[str, Any]] = None,
+               out: Optional[DeviceArray] = None,
+               acc: Optional[DeviceArray] = None) -> DeviceArray:
+    """Per-token int8 activation codes times int8 weights, int32
+    accumulation (``acc`` receives the accumulators when given)."""
+    if x.dtype != np.float32:
+        raise NotImplementedError(f"W8A8 Dense takes float32 activations, got {x.dtype}")
+    m, k = _rows(x)
+    n, wk = w.shape[-2], w.shape[-1]
+    if wk != k:
+        raise ValueError(f"shapes {x.shape} and {w.shape} not aligned: {k} (dim -1) != {wk}")
+    code, alpha, clip = activation_args(activation, activation_params)
+    y = out if out is not None else DeviceArray(x.shape[:-1] + (n,), np.float32)
+    _lib.call("enq_dense_w8a8", x.ptr, m, k, w.codes.ptr, w.scale.ptr, n,
+              bias.ptr if bias is not None else null(), code, alpha, clip, y.ptr,
+              acc.ptr if acc is not None else null())
+    return y
+
+
+def quantize_rows_i8(x: DeviceArray) -> Tuple[DeviceArray, DeviceArray]:
+    """Per-row (per-token) symmetric int8 codes and fp32 scales."""
+    m, k = _rows(x)
+    codes = DeviceArray(x.shape, np.int8)
+    scale = DeviceArray((m,), np.float32)
+    _lib.call("enq_quantize_rows_i8", x.ptr, m, k, codes.ptr, scale.ptr)
+    return codes, scale
+
+
+def gemm_w8a8(x_codes: DeviceArray, x_scale: DeviceArray, w: Int8Weights,
+              bias: Optional[DeviceArray] = None, activation: str = "linear",
+              out: Optional[DeviceArray] = None,
+              acc: Optional[DeviceArray] = None) -> DeviceArray:
+    """The integer GEMM on already-quantized activations."""
+    m, k = _rows(x_codes)
+    n = w.shape[-2]
+    code, alpha, clip = activation_args(activation)
+    y = out if out is not None else DeviceArray(x_codes.shape[:-1] + (n,), np.float32)
+    _lib.call("enq_gemm_w8a8", x_codes.ptr, x_scale.ptr, w.codes.ptr, w.scale.ptr,
+              bias.ptr if bias is not None else null(), m, n, k, code, alpha, clip, y.ptr,
+              acc.ptr if acc is not None else null())
+    return y
+
+
+def quantize_weight_rows(w: np.ndarray) -> Int8Weights:
+    """Per-output-channel symmetric int8 codes of a float32 ``(n, k)`` weight
+    on the device (``quantize_tensor(w, 8, per_channel=True)`` semantics)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    if w.ndim != 2:
+        raise ValueError(f"expected a 2-D weight, got shape {w.shape}")
+    d_w = DeviceArray.from_numpy(w)
+    codes, scale = quantize_rows_i8(d_w)
+    return Int8Weights(codes, scale, w.shape, 8, True, None, None)

@@ -1,0 +1,91 @@
+"""Drop-in ``Forward`` for quantized models on MI355X.
+
+Mirrors ``Enilnets/nn/forward.py:272-811`` for the layer types of the
+quantized-inference path: the input is cast to float32 (the reference's
+default working dtype, ``:285``), every layer runs on the device, and
+``model.outputs`` / ``model.pre_activations`` are filled with host arrays as
+the reference fills them (``:295-302,810``).  Dense layers run on their int8
+codes (``enilnets_amd.nn.weights``).  Layer types outside this path raise
+NotImplementedError instead of silently computing on the host.
+"""
+
+from typing import Any, Dict, List, Optional
+
+import numpy as np
+
+from .. import _lib
+from ..device import DeviceArray
+from .dense import dense_w8
+from .weights import int8_weights
+
+#: Activations whose NumPy result is float64 for a float32 input, because
+#: ``activations.py:32`` multiplies by ``np.sqrt(2 / np.pi)`` (a float64
+#: NumPy scalar) and NumPy 2 promotes the result.
+_FLOAT64_ACTIVATIONS = {"gelu"}
+
+
+def _bias(layer: Dict[str, Any], key: str, n: int) -> DeviceArray:
+    b = layer.get(key)
+    if b is None:
+        b = np.zeros(n, np.float32)
+    return DeviceArray.from_numpy(np.ascontiguousarray(b, dtype=np.float32))
+
+
+def _fake_quantize_device(x: DeviceArray, spec: Dict[str, Any]) -> DeviceArray:
+    """``act_quant`` (``forward.py:798-805``): per-tensor fake quantization
+    of a layer output with the calibrated scale and zero point."""
+    from ..compression.quantization import quant_range
+    qmin, qmax = quant_range(spec["bits"], spec["scheme"])
+    scale = np.asarray(spec["scale"])
+    zp = np.asarray(spec["zero_point"])
+    if scale.size != 1 or zp.size != 1:
+        raise NotImplementedError("act_quant specs are per tensor")
+    d_s = DeviceArray.from_numpy(scale.reshape(1).astype(np.float32))
+    d_z = DeviceArray.from_numpy(zp.reshape(1).astype(np.float32))
+    out = DeviceArray(x.shape, np.float32)
+    _lib.call("enq_fake_quantize", _lib.F32, x.ptr, 1, 1, x.size, d_s.ptr, d_z.ptr, qmin, qmax,
+              out.ptr)
+    return out
+
+
+def Forward(model: Any, inputs: Any, training: bool = False, dropout_rate: float = 0.0,
+            variant: str = "fp32") -> np.ndarray:
+    """Run ``inputs`` through ``model.layers`` on the GPU.  Returns the last
+    layer's output and fills ``model.outputs`` and ``model.pre_activations``
+    like the reference.  ``variant`` selects the W8 Dense arithmetic
+    ("fp32": fp32-accurate, "bf16": bf16 activations)."""
+    x = np.asarray(inputs, dtype=np.float32)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    outputs: List[np.ndarray] = [x]
+    pre: List[Optional[np.ndarray]] = [None]
+    dev: List[DeviceArray] = [DeviceArray.from_numpy(x)]
+    for layer in model.layers:
+        cur = dev[-1]
+        kind = layer["type"]
+        z_host = None
+        if kind in ("dense", "sparse"):
+            w = int8_weights(layer, "weights")
+            n = w.shape[0]
+            z = DeviceArray(cur.shape[:-1] + (n,), np.float32)
+            y = dense_w8(cur, w, _bias(layer, "bias", n), layer["activation"],
+                         layer.get("activation_params", {}), variant, pre_activation=z)
+            z_host = z.numpy()
+            host = y.numpy()
+            if layer["activation"] in _FLOAT64_ACTIVATIONS:
+                host = host.astype(np.float64)
+        elif kind == "residual_save":
+            y, host = cur, outputs[-1]
+        else:
+            raise NotImplementedError(
+                f"layer type {kind!r} is not on enilnets_amd's quantized path")
+        spec = layer.get("act_quant")
+        if spec is not None:
+            y = _fake_quantize_device(y, spec)
+            host = y.numpy().astype(host.dtype, copy=False)
+        dev.append(y)
+        outputs.append(host)
+        pre.append(z_host)
+    model.outputs = outputs
+    model.pre_activations = pre
+    return outputs[-1]

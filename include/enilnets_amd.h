@@ -1,0 +1,224 @@
+/*
+ * enilnets_amd.h -- C ABI of libenilnets_amd.so, the MI355X (gfx950)
+ * implementation of Enilnets' quantized-inference hot path.
+ *
+ * The reference (Enilnets v4.11.0) is pure NumPy and has no FFI; the path sits
+ * behind the module functions of Enilnets/compression/quantization.py and the
+ * Dense branch of Enilnets/nn/forward.py.  Each entry point below names the
+ * reference expression it replaces (path:line under the reference tree).
+ *
+ * Conventions
+ *   - Every function returns an int status: ENQ_OK (0) or one of the
+ *     ENQ_ERR_* codes.  enq_last_error() gives the message of the last failure
+ *     on the calling thread.
+ *   - Array arguments are DEVICE pointers (from enq_malloc or any other HIP
+ *     allocation on the current device) unless the name says "host".
+ *   - Kernels are enqueued on the library stream (enq_get_stream /
+ *     enq_set_stream) and return before they finish; enq_synchronize() waits.
+ *     The copy functions are synchronous.
+ *   - Tensors are dense and row-major.  A per-channel tensor is described as
+ *     (outer, channels, inner): element (o, c, i) sits at (o*channels + c)*inner
+ *     + i and belongs to channel c.  A per-tensor operation is channels == 1.
+ *   - Weights are (n_out, n_in) as in Enilnets/nn/weight_init.py:13-14, so the
+ *     Dense GEMM is y = x . W^T + b (Enilnets/nn/forward.py:318-319).
+ */
+#ifndef ENILNETS_AMD_H
+#define ENILNETS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ENQ_ABI_VERSION 1
+
+/* status codes */
+#define ENQ_OK 0
+#define ENQ_ERR_INVALID 1     /* bad argument: maps to ValueError          */
+#define ENQ_ERR_RUNTIME 2     /* HIP runtime failure: maps to RuntimeError */
+#define ENQ_ERR_NO_DEVICE 3   /* no usable gfx950 device: RuntimeError     */
+#define ENQ_ERR_UNSUPPORTED 4 /* valid but not implemented: NotImplementedError */
+
+/* element types of float tensors */
+#define ENQ_F32 0
+#define ENQ_F64 1
+
+/* quantization schemes, Enilnets/compression/quantization.py:25-28 */
+#define ENQ_SYMMETRIC 0
+#define ENQ_ASYMMETRIC 1
+
+/* activations, Enilnets/nn/activations.py:21-41 */
+#define ENQ_ACT_LINEAR 0
+#define ENQ_ACT_RELU 1
+#define ENQ_ACT_LEAKYRELU 2
+#define ENQ_ACT_ELU 3
+#define ENQ_ACT_SELU 4
+#define ENQ_ACT_GELU 5
+#define ENQ_ACT_SWISH 6
+#define ENQ_ACT_MISH 7
+#define ENQ_ACT_SIGMOID 8
+#define ENQ_ACT_TANH 9
+#define ENQ_ACT_SOFTPLUS 10
+#define ENQ_ACT_SOFTMAX 11
+
+/* W8 Dense arithmetic variants */
+#define ENQ_W8_FP32 0 /* fp32-accurate: activations split into bf16 hi+lo   */
+#define ENQ_W8_BF16 1 /* activations rounded to bf16 once                    */
+
+typedef struct enq_device_info {
+  char name[128];
+  char arch[64];         /* e.g. "gfx950:sramecc+:xnack-" */
+  int device;
+  int compute_units;
+  int clock_khz;
+  int memory_clock_khz;
+  int memory_bus_width;
+  int l2_bytes;
+  int lds_bytes_per_block;
+  int wavefront_size;
+  long long global_memory_bytes;
+} enq_device_info;
+
+/* ---- lifecycle ------------------------------------------------------- */
+int enq_abi_version(void);
+/* Select `device`, check it is gfx950, create the library stream. */
+int enq_init(int device);
+int enq_get_device_info(enq_device_info* out);
+int enq_synchronize(void);
+const char* enq_last_error(void);
+/* The stream kernels are launched on (a hipStream_t). */
+int enq_get_stream(void** stream);
+/* Launch on a caller-owned stream instead (NULL restores the library's). */
+int enq_set_stream(void* stream);
+
+/* ---- device memory -------------------------------------------------- */
+int enq_malloc(void** dptr, size_t bytes);
+int enq_free(void* dptr);
+int enq_copy_to_device(void* dst, const void* host_src, size_t bytes);
+int enq_copy_to_host(void* host_dst, const void* src, size_t bytes);
+int enq_copy_on_device(void* dst, const void* src, size_t bytes);
+
+/* ---- timing (HIP events recorded on the library stream) ----------- */
+int enq_event_create(void** event);
+int enq_event_destroy(void* event);
+int enq_event_record(void* event);
+int enq_event_elapsed_ms(void* start, void* end, float* ms);
+
+/* ---- quantization primitives ---------------------------------------
+ * dtype is ENQ_F32 or ENQ_F64 for x, scale, zero_point, low, high and the
+ * float outputs.  qmin/qmax come from quant_range
+ * (Enilnets/compression/quantization.py:21-30).
+ */
+
+/* Per-channel min and max (NaN-propagating like np.min/np.max).
+ * Replaces np.min/np.max(w, axis=all-but-axis, keepdims=True) and the global
+ * np.min(w)/np.max(w) of quantize_tensor, quantization.py:86-91.
+ * low/high hold `channels` values. */
+int enq_minmax(int dtype, const void* x, int64_t outer, int64_t channels,
+               int64_t inner, void* low, void* high);
+
+/* Elementwise scale and zero point from ranges.
+ * Replaces compute_scale, quantization.py:33-50. */
+int enq_compute_scale(int dtype, const void* low, const void* high, int64_t n,
+                      int bits, int scheme, void* scale, void* zero_point);
+
+/* codes = clip(round_half_even(x / scale + zero_point), qmin, qmax), as floats
+ * of `dtype`.  Replaces quantize, quantization.py:53-56.  scale/zero_point hold
+ * `channels` values. */
+int enq_quantize(int dtype, const void* x, int64_t outer, int64_t channels,
+                 int64_t inner, const void* scale, const void* zero_point,
+                 int qmin, int qmax, void* codes);
+
+/* The codes of enq_quantize stored as int8 (NaN -> 0): quantize,
+ * quantization.py:53-56, with a given scale.  Requires -128 <= qmin <= qmax
+ * <= 127.  Used to rebuild int8 weight codes from fake-quantized floats and
+ * their stored scale. */
+int enq_quantize_codes_i8(int dtype, const void* x, int64_t outer,
+                          int64_t channels, int64_t inner, const void* scale,
+                          const void* zero_point, int qmin, int qmax,
+                          int8_t* codes);
+
+/* out = (q - zero_point) * scale.  Replaces dequantize, quantization.py:59-61. */
+int enq_dequantize(int dtype, const void* q, int64_t outer, int64_t channels,
+                   int64_t inner, const void* scale, const void* zero_point,
+                   void* out);
+
+/* dequantize(quantize(x)).  Replaces fake_quantize, quantization.py:64-69. */
+int enq_fake_quantize(int dtype, const void* x, int64_t outer, int64_t channels,
+                      int64_t inner, const void* scale, const void* zero_point,
+                      int qmin, int qmax, void* out);
+
+/* Fused quantize_tensor: statistics, scale, zero point and the fake-quantized
+ * tensor in one call.  Replaces quantize_tensor, quantization.py:76-93
+ * (channels == 1 is the per-tensor branch :90-91).
+ *   out_fake   (nullable) fake-quantized tensor of `dtype`
+ *   out_codes  (nullable) the same codes as int8; requires qmin >= -128 and
+ *              qmax <= 127; a NaN element gets code 0
+ *   scale, zero_point  `channels` values of `dtype`
+ *   abs_err    (nullable) one double: sum |fake - w| over the tensor, the
+ *              numerator of quantize_weights' mean_abs_error (:137) */
+int enq_quantize_tensor(int dtype, const void* w, int64_t outer,
+                        int64_t channels, int64_t inner, int bits, int scheme,
+                        void* out_fake, int8_t* out_codes, void* scale,
+                        void* zero_point, double* abs_err);
+
+/* Symmetric 8-bit per-row quantization of fp32 rows to int8 codes plus one
+ * fp32 scale per row: quantize_tensor(x, 8, "symmetric", per_channel=True)
+ * (quantization.py:76-93) with the codes kept as int8.  Used for the
+ * per-output-channel weight codes and for per-token activation codes. */
+int enq_quantize_rows_i8(const float* x, int64_t rows, int64_t cols,
+                         int8_t* codes, float* scale);
+
+/* Int8 codes back to floats: out = code * scale, scale per channel.
+ * Replaces dequantize (quantization.py:59-61) for symmetric int8 storage. */
+int enq_dequantize_i8(int dtype, const int8_t* codes, int64_t outer,
+                      int64_t channels, int64_t inner, const void* scale,
+                      void* out);
+
+/* Sums for quantization_error (quantization.py:218-229) over n elements:
+ * out[0] = sum|b-a|, out[1] = max|b-a|, out[2] = sum a*a, out[3] = sum (b-a)^2,
+ * accumulated in double. */
+int enq_error_stats(int dtype, const void* reference, const void* candidate,
+                    int64_t n, double* host_out4);
+
+/* ---- Dense on int8 weights -----------------------------------------
+ * y = act(x . (codes * w_scale)^T + bias) with x (m, k) fp32, codes (n, k)
+ * int8, w_scale (n) fp32, bias (n) fp32 or NULL, y (m, n) fp32.
+ * Replaces the Dense branch z = np.dot(x, W.T) + b; activate(z),
+ * Enilnets/nn/forward.py:318-321 with W the fake-quantized weights (which
+ * equal codes * scale to within one fp32 rounding).  z (nullable) receives the
+ * pre-activation.  act_alpha is the leakyrelu/elu alpha, act_clip the
+ * sigmoid/softplus clip (activations.py:20-37).  Small m runs the split-K
+ * GEMV kernel, larger m the LDS-tiled MFMA GEMM. */
+int enq_dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes,
+                 const float* w_scale, int64_t n, const float* bias,
+                 int activation, float act_alpha, float act_clip, int variant,
+                 float* y, float* z);
+
+/* W8A8: int8 activation codes (m, k) with one fp32 scale per row, int8
+ * weight codes (n, k) with one fp32 scale per row of W.
+ * acc = x_codes . w_codes^T (int32, exact); y = act(acc * x_scale * w_scale + b).
+ * acc (nullable) receives the int32 accumulators.  The reference has no
+ * integer GEMM (quantization.py:1-14); this is the composition of its
+ * quantize_tensor (:76-93) with the Dense branch (forward.py:318-321). */
+int enq_gemm_w8a8(const int8_t* x_codes, const float* x_scale,
+                  const int8_t* w_codes, const float* w_scale,
+                  const float* bias, int64_t m, int64_t n, int64_t k,
+                  int activation, float act_alpha, float act_clip, float* y,
+                  int32_t* acc);
+
+/* W8A8 Dense from fp32 activations: per-token quantization
+ * (enq_quantize_rows_i8) followed by enq_gemm_w8a8, using the library
+ * workspace for the activation codes. */
+int enq_dense_w8a8(const float* x, int64_t m, int64_t k, const int8_t* codes,
+                   const float* w_scale, int64_t n, const float* bias,
+                   int activation, float act_alpha, float act_clip, float* y,
+                   int32_t* acc);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ENILNETS_AMD_H */

@@ -1,0 +1,134 @@
+"""GPU parity of the Dense kernels on int8 weights.
+
+* W8 fp32 variant: max |z - z_ref| <= 1e-4 * max |z_ref| per row, where z_ref
+  is the float64 product of the activations with the fake-quantized weights
+  (the reference's Dense, ``nn/forward.py:318-319``).
+* W8 bf16 variant: the same bound at 2e-2.
+* W8A8: int32 accumulators, activation codes and scales bit-identical to the
+  oracle; the linear fp32 output too (same operation order, no FMA).
+"""
+
+import numpy as np
+import pytest
+
+from enilnets_amd.device import DeviceArray
+from enilnets_amd.nn import dense as D
+from enilnets_amd.nn.weights import Int8Weights
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def make(m, k, n, seed, per_channel=True, wstd=0.05):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * wstd).astype(np.float32)
+    b = (rng.standard_normal(n) * 0.01).astype(np.float32)
+    fq, scale, _ = oracle.quantize_tensor(w, 8, per_channel=per_channel)
+    codes = oracle.quantize(w, scale, np.zeros_like(scale), 8, "symmetric").astype(np.int8)
+    rows = np.broadcast_to(np.asarray(scale, np.float32).reshape(-1, 1)[:, 0]
+                           if np.ndim(scale) else np.full(n, scale, np.float32), (n,))
+    wq = Int8Weights(DeviceArray.from_numpy(codes), DeviceArray.from_numpy(np.ascontiguousarray(rows)),
+                     codes.shape, 8, per_channel, None, None)
+    return x, fq, codes, np.ascontiguousarray(rows), b, wq
+
+
+def row_rel_err(got, ref):
+    denom = np.maximum(np.max(np.abs(ref), axis=-1), 1e-30)
+    return np.max(np.abs(got - ref), axis=-1) / denom
+
+
+SHAPES = [(1, 512, 512), (3, 100, 10), (16, 8192, 1024), (16, 784, 1024), (17, 1024, 300),
+          (33, 512, 100), (64, 512, 512), (65, 784, 1024), (100, 100, 37), (256, 1024, 1024),
+          (300, 784, 1024), (512, 4096, 1024), (1000, 1024, 10), (4, 16, 1), (129, 48, 260)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+@pytest.mark.parametrize("variant,tol", [("fp32", 1e-4), ("bf16", 2e-2)])
+def test_dense_w8_pre_activation(gpu, m, k, n, variant, tol):
+    print(f"[case] dense_w8 {variant} m={m} k={k} n={n}", flush=True)
+    x, fq, codes, rows, b, wq = make(m, k, n, seed=m * 31 + k + n)
+    z_ref = x.astype(np.float64) @ fq.astype(np.float64).T + b
+    d_x, d_b = DeviceArray.from_numpy(x), DeviceArray.from_numpy(b)
+    z = DeviceArray((m, n), np.float32)
+    y = D.dense_w8(d_x, wq, d_b, "linear", variant=variant, pre_activation=z)
+    zh, yh = z.numpy(), y.numpy()
+    assert np.array_equal(zh, yh)
+    err = row_rel_err(zh.astype(np.float64), z_ref)
+    assert np.all(err <= tol), f"max row error {err.max():.3e} > {tol}"
+
+
+def test_dense_w8_large_gemv_and_gemm(gpu):
+    # BASELINE config 3 shapes; rows of the GEMM checked on a sample
+    for m in (16, 4096):
+        print(f"[case] dense_w8 fp32 m={m} k=8192 n=8192", flush=True)
+        x, fq, codes, rows, b, wq = make(m, 8192, 8192, seed=m, wstd=0.02)
+        y = D.dense_w8(DeviceArray.from_numpy(x), wq, None, "linear").numpy()
+        pick = np.random.default_rng(0).choice(m, size=min(m, 48), replace=False)
+        ref = x[pick].astype(np.float64) @ fq.astype(np.float64).T
+        assert np.all(row_rel_err(y[pick].astype(np.float64), ref) <= 1e-4)
+
+
+@pytest.mark.parametrize("act", ["relu", "leakyrelu", "elu", "selu", "gelu", "swish", "mish",
+                                 "sigmoid", "tanh", "softplus", "softmax"])
+def test_dense_w8_activations(gpu, act):
+    print(f"[case] activation {act}", flush=True)
+    x, fq, codes, rows, b, wq = make(96, 256, 130, seed=7)
+    z = DeviceArray((96, 130), np.float32)
+    y = D.dense_w8(DeviceArray.from_numpy(x), wq, DeviceArray.from_numpy(b), act,
+                   pre_activation=z).numpy()
+    zh = z.numpy()
+    want = oracle.activate(act, zh.astype(np.float64))
+    assert np.allclose(y, want, rtol=2e-6, atol=2e-6)
+
+
+def test_dense_w8_rejects_bad_shapes(gpu):
+    x, fq, codes, rows, b, wq = make(4, 32, 8, seed=1)
+    with pytest.raises(ValueError):
+        D.dense_w8(DeviceArray.from_numpy(np.zeros((4, 31), np.float32)), wq)
+    with pytest.raises(ValueError):
+        D.dense_w8(DeviceArray.from_numpy(x), wq, activation="bogus")
+
+
+W8A8_SHAPES = [(1, 64, 64), (7, 100, 33), (16, 8192, 512), (64, 784, 1024), (200, 1000, 300),
+               (256, 1024, 1024), (512, 4096, 1024), (1000, 48, 10), (130, 16, 70),
+               (4096, 1024, 4096)]
+
+
+@pytest.mark.parametrize("m,k,n", W8A8_SHAPES)
+def test_w8a8_bit_exact(gpu, m, k, n):
+    print(f"[case] w8a8 m={m} k={k} n={n}", flush=True)
+    x, fq, codes, rows, b, wq = make(m, k, n, seed=m + k * 3 + n)
+    y_ref, acc_ref, xs_ref, xc_ref = oracle.w8a8_dense(x, codes, rows, b)
+    d_x = DeviceArray.from_numpy(x)
+    xc, xs = D.quantize_rows_i8(d_x)
+    assert np.array_equal(xc.numpy(), xc_ref)
+    assert np.array_equal(xs.numpy(), xs_ref.reshape(-1))
+    acc = DeviceArray((m, n), np.int32)
+    y = D.dense_w8a8(d_x, wq, DeviceArray.from_numpy(b), "linear", acc=acc)
+    assert np.array_equal(acc.numpy(), acc_ref)
+    assert np.array_equal(y.numpy(), y_ref)
+    acc2 = DeviceArray((m, n), np.int32)
+    y2 = D.gemm_w8a8(xc, xs, wq, DeviceArray.from_numpy(b), acc=acc2)
+    assert np.array_equal(acc2.numpy(), acc_ref)
+    assert np.array_equal(y2.numpy(), y_ref)
+
+
+def test_w8a8_square_8192(gpu):
+    print("[case] w8a8 8192^3", flush=True)
+    rng = np.random.default_rng(77)
+    xc = rng.integers(-127, 128, (8192, 8192), dtype=np.int8)
+    wc = rng.integers(-127, 128, (8192, 8192), dtype=np.int8)
+    xs = np.full(8192, 0.01, np.float32)
+    ws = np.full(8192, 0.02, np.float32)
+    wq = Int8Weights(DeviceArray.from_numpy(wc), DeviceArray.from_numpy(ws), wc.shape, 8, True,
+                     None, None)
+    acc = DeviceArray((8192, 8192), np.int32)
+    D.gemm_w8a8(DeviceArray.from_numpy(xc), DeviceArray.from_numpy(xs), wq, acc=acc)
+    got = acc.numpy()
+    pick = rng.choice(8192, size=24, replace=False)
+    want = (xc[pick].astype(np.float64) @ wc.astype(np.float64).T).astype(np.int64)
+    assert np.array_equal(got[pick].astype(np.int64), want)
+    # a checksum of all rows: sum over n of acc equals x . (sum of W rows)
+    wsum = wc.astype(np.int64).sum(axis=0)
+    assert np.array_equal(got.astype(np.int64).sum(axis=1), xc.astype(np.int64) @ wsum)

@@ -1,0 +1,362 @@
+"""Pins the NumPy oracle (``oracle/``) before it is trusted as the checker.
+
+Three kinds of evidence, none of which re-types the oracle's own formula:
+
+1. the reference's own quantization tests (``test_enilnets.py:11133-11243``)
+   and its MoE dense-mixture oracle (``:8331-8353``), ported as invariants;
+2. an independent exact-arithmetic model: Python ``Fraction`` division with
+   explicit round-to-nearest-even to float32 / float64, and Python's
+   half-even ``round`` for the codes;
+3. brute force around the half-way points ``(k + 1/2) * scale``, with
+   planted mistakes (reciprocal multiply, round-half-away, a dropped
+   ``+ zero_point``, a transposed weight) that must be caught.
+"""
+
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import oracle
+
+
+# ---------------------------------------------------------------------------
+# exact arithmetic helpers (independent of NumPy's ufuncs)
+# ---------------------------------------------------------------------------
+def round_fraction(q: Fraction, mant_bits: int, emin: int) -> float:
+    """Round a rational to the nearest binary float with ``mant_bits``
+    significand bits (ties to even); subnormals below ``2**emin``."""
+    if q == 0:
+        return 0.0
+    sign = -1.0 if q < 0 else 1.0
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    ulp_exp = max(e, emin) - (mant_bits - 1)
+    scaled = a / (Fraction(2) ** ulp_exp)
+    n = scaled.numerator // scaled.denominator
+    rem = scaled - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return sign * float(Fraction(n) * Fraction(2) ** ulp_exp)
+
+
+def rn32(q: Fraction) -> float:
+    return round_fraction(q, 24, -126)
+
+
+def rn64(q: Fraction) -> float:
+    return round_fraction(q, 53, -1022)
+
+
+def exact_scale(amax: float, qmax: int, rn) -> float:
+    return rn(Fraction(amax) / qmax) if amax > 0 else 1.0
+
+
+def exact_code(x: float, s: float, rn, qmin=-127, qmax=127) -> float:
+    v = rn(Fraction(x) / Fraction(s))
+    return float(min(max(round(v), qmin), qmax))
+
+
+# ---------------------------------------------------------------------------
+# 1. the reference's own invariants (test_enilnets.py:11133-11243)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("scheme", ["symmetric", "asymmetric"])
+def test_grid_round_trip_half_step(scheme):
+    # test_enilnets.py:11133-11145
+    x = np.linspace(-3.0, 5.0, 101)
+    scale, zp = oracle.compute_scale(np.min(x), np.max(x), 8, scheme)
+    q = oracle.quantize(x, scale, zp, 8, scheme)
+    assert np.all(q == np.round(q))
+    back = oracle.dequantize(q, scale, zp)
+    assert float(np.max(np.abs(back - x))) <= float(np.max(scale)) * 0.5 + 1e-9
+
+
+def test_symmetric_keeps_exact_zeros():
+    # test_enilnets.py:11147-11153
+    rng = np.random.default_rng(1)
+    x = np.concatenate([np.zeros(50), rng.standard_normal(50)])
+    q, _, _ = oracle.quantize_tensor(x, bits=8, scheme="symmetric")
+    assert np.all(q[:50] == 0)
+
+
+def test_more_bits_less_error():
+    # test_enilnets.py:11155-11160
+    x = np.random.default_rng(2).standard_normal(500)
+    errors = [float(np.mean(np.abs(oracle.quantize_tensor(x, bits=b)[0] - x)))
+              for b in (4, 6, 8, 12)]
+    assert errors == sorted(errors, reverse=True)
+
+
+def test_per_channel_beats_per_tensor():
+    # test_enilnets.py:11162-11177
+    w = np.random.default_rng(3).standard_normal((8, 16)) * 0.01
+    w[0] = w[0] * 1000.0
+    pt = oracle.quantize_tensor(w, 8, per_channel=False)[0]
+    pc = oracle.quantize_tensor(w, 8, per_channel=True)[0]
+    err_pt = float(np.mean(np.abs(pt[1:] - w[1:])))
+    err_pc = float(np.mean(np.abs(pc[1:] - w[1:])))
+    assert err_pc < err_pt / 50
+    assert float(np.mean(np.abs(pc - w))) <= float(np.mean(np.abs(pt - w)))
+
+
+def _mlp(rng, dtype=np.float32):
+    class M:
+        pass
+    m = M()
+    w1 = (rng.standard_normal((32, 20)) * 0.3).astype(dtype)
+    w2 = (rng.standard_normal((4, 32)) * 0.3).astype(dtype)
+    m.layers = [
+        {"type": "dense", "weights": w1, "bias": np.zeros(32, dtype), "activation": "relu",
+         "use_bias": True, "activation_params": {}},
+        {"type": "dense", "weights": w2, "bias": np.zeros(4, dtype), "activation": "softmax",
+         "use_bias": True, "activation_params": {}},
+    ]
+    return m
+
+
+def test_quantize_weights_report_and_error():
+    # test_enilnets.py:11179-11199
+    import copy
+    rng = np.random.default_rng(4)
+    m = _mlp(rng)
+    X = rng.standard_normal((64, 20)).astype(np.float32)
+    ref = [oracle.forward(m.layers, X)[-1]]
+    errors = {}
+    for bits in (8, 4):
+        mm = copy.deepcopy(m)
+        report = oracle.quantize_weights(mm, bits=bits)
+        assert report["bits"] == bits
+        assert report["parameters"] == 32 * 20 + 4 * 32
+        assert report["compression"] == pytest.approx(32 / bits, abs=1e-6)
+        assert report["quantized_bytes"] == report["parameters"] * bits // 8
+        errors[bits] = oracle.quantization_error(ref, [oracle.forward(mm.layers, X)[-1]])[
+            "relative_error"]
+    assert errors[8] < errors[4]
+    assert errors[8] < 1e-2
+
+
+def test_codes_on_grid():
+    # test_enilnets.py:11201-11210
+    rng = np.random.default_rng(5)
+    m = _mlp(rng)
+    oracle.quantize_weights(m, bits=8, scheme="symmetric")
+    spec = m.layers[0]["quant"]["weights"]
+    codes = m.layers[0]["weights"] / spec["scale"]
+    assert np.all(np.abs(codes - np.round(codes)) < 1e-4)
+
+
+def test_quant_range_and_validation():
+    # test_enilnets.py:11236-11243
+    assert oracle.quant_range(8, "symmetric") == (-127, 127)
+    assert oracle.quant_range(8, "asymmetric") == (0, 255)
+    assert oracle.quant_range(2, "symmetric") == (-1, 1)
+    assert oracle.quant_range(16, "asymmetric") == (0, 65535)
+    for bad in ((1, "symmetric"), (17, "symmetric"), (8, "bogus")):
+        with pytest.raises(ValueError):
+            oracle.quant_range(*bad)
+
+
+# ---------------------------------------------------------------------------
+# 2. exact arithmetic
+# ---------------------------------------------------------------------------
+def test_symmetric_per_tensor_matches_exact_arithmetic_f32():
+    rng = np.random.default_rng(6)
+    w = (rng.standard_normal((7, 13)) * 0.05).astype(np.float32)
+    fq, scale, zp = oracle.quantize_tensor(w, 8)
+    amax = max(abs(float(w.min())), abs(float(w.max())))
+    s = exact_scale(amax, 127, rn32)
+    assert float(scale) == s
+    assert scale.dtype == np.float32 and scale.shape == ()
+    assert zp.dtype == np.float32 and float(zp) == 0.0
+    for xi, fi in zip(w.reshape(-1), fq.reshape(-1)):
+        c = exact_code(float(xi), s, rn32)
+        assert float(fi) == rn32(Fraction(c) * Fraction(s))
+
+
+def test_symmetric_per_channel_matches_exact_arithmetic_f64():
+    rng = np.random.default_rng(7)
+    w = rng.standard_normal((5, 9)) * 3.0
+    fq, scale, _ = oracle.quantize_tensor(w, 8, per_channel=True)
+    assert scale.shape == (5, 1) and scale.dtype == np.float64 and fq.dtype == np.float64
+    for r in range(5):
+        amax = float(np.max(np.abs(w[r])))
+        s = exact_scale(amax, 127, rn64)
+        assert float(scale[r, 0]) == s
+        for xi, fi in zip(w[r], fq[r]):
+            c = exact_code(float(xi), s, rn64)
+            assert float(fi) == rn64(Fraction(c) * Fraction(s))
+
+
+def test_asymmetric_matches_exact_arithmetic():
+    rng = np.random.default_rng(8)
+    w = (rng.uniform(-0.3, 2.0, (4, 6))).astype(np.float32)
+    fq, scale, zp = oracle.quantize_tensor(w, 8, "asymmetric")
+    low, high = float(w.min()), float(w.max())
+    span = rn32(Fraction(high) - Fraction(low))
+    s = rn32(Fraction(span) / 255)
+    z = float(round(rn32(0 - Fraction(rn32(Fraction(low) / Fraction(s))))))
+    assert float(scale) == s and float(zp) == z
+    for xi, fi in zip(w.reshape(-1), fq.reshape(-1)):
+        v = rn32(Fraction(rn32(Fraction(float(xi)) / Fraction(s))) + Fraction(z))
+        c = min(max(round(v), 0), 255)
+        assert float(fi) == rn32(Fraction(rn32(Fraction(c) - Fraction(z))) * Fraction(s))
+
+
+def test_zero_range_gives_unit_scale_and_nan_propagates():
+    fq, scale, _ = oracle.quantize_tensor(np.zeros((3, 4), np.float32), 8, per_channel=True)
+    assert np.all(scale == 1.0) and np.all(fq == 0)
+    w = np.array([1.0, np.nan, -2.0], np.float32)
+    fq, scale, _ = oracle.quantize_tensor(w, 8)
+    # amax is NaN, NaN > 0 is False -> scale 1 (quantization.py:44)
+    assert float(scale) == 1.0
+    assert np.isnan(fq[1]) and fq[0] == 1.0 and fq[2] == -2.0
+
+
+def test_signed_zero_semantics():
+    # x / s + 0.0 turns -0.0 into +0.0 before rounding; small negatives
+    # still round to -0.0 and dequantize to -0.0.
+    s = np.float32(0.1)
+    zp = np.float32(0.0)
+    q = oracle.quantize(np.array([-0.0, -0.01, 0.01], np.float32), s, zp, 8, "symmetric")
+    assert not np.signbit(q[0]) and np.signbit(q[1]) and not np.signbit(q[2])
+    f = oracle.dequantize(q, s, zp)
+    assert not np.signbit(f[0]) and np.signbit(f[1])
+
+
+def test_codes_bounds_and_extreme_hit():
+    rng = np.random.default_rng(9)
+    for _ in range(20):
+        w = (rng.standard_normal((16, 33)) * rng.uniform(1e-3, 10)).astype(np.float32)
+        codes, scale = oracle.int8_codes(w, per_channel=True)
+        assert codes.dtype == np.int8
+        assert np.all(np.abs(codes.astype(np.int32)) <= 127)
+        assert np.all(np.max(np.abs(codes.astype(np.int32)), axis=1) == 127)
+
+
+# ---------------------------------------------------------------------------
+# 3. brute force at the half-way points, with planted mistakes
+# ---------------------------------------------------------------------------
+def _halfway_inputs(seed=10, n_scales=12):
+    rng = np.random.default_rng(seed)
+    xs, ss = [], []
+    for _ in range(n_scales):
+        s = np.float32(rng.uniform(1e-3, 1.0) / 127)
+        for k in range(-127, 127):
+            t = np.float32(float((Fraction(k) + Fraction(1, 2)) * Fraction(float(s))))
+            x = t
+            for _ in range(2):
+                x = np.nextafter(x, np.float32(-np.inf))
+            for _ in range(5):
+                xs.append(x)
+                ss.append(s)
+                x = np.nextafter(x, np.float32(np.inf))
+    return np.array(xs, np.float32), np.array(ss, np.float32)
+
+
+def _exact_codes(xs, ss):
+    return np.array([exact_code(float(x), float(s), rn32) for x, s in zip(xs, ss)], np.float32)
+
+
+def test_halfway_points_match_exact_rounding():
+    xs, ss = _halfway_inputs()
+    got = oracle.quantize(xs, ss, np.zeros_like(ss), 8, "symmetric")
+    want = _exact_codes(xs, ss)
+    assert np.array_equal(got, want)
+
+
+def test_planted_mistakes_are_caught():
+    xs, ss = _halfway_inputs()
+    want = _exact_codes(xs, ss)
+    # reciprocal multiply instead of division
+    recip = np.clip(np.round(xs * (np.float32(1) / ss)), -127, 127)
+    # round half away from zero instead of half to even
+    away = np.clip(np.trunc(xs / ss + np.copysign(np.float32(0.5), xs / ss)), -127, 127)
+    assert not np.array_equal(recip, want)
+    assert not np.array_equal(away, want)
+    # a dropped "+ zero_point" changes the sign of zero codes
+    q = oracle.quantize(np.array([-0.0], np.float32), np.float32(1), np.float32(0), 8,
+                        "symmetric")
+    assert not np.signbit(q[0]) and np.signbit(np.round(np.float32(-0.0) / np.float32(1)))
+
+
+# ---------------------------------------------------------------------------
+# Dense / W8A8 / MoE / activations
+# ---------------------------------------------------------------------------
+def test_w8a8_accumulator_is_the_exact_integer_dot():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((5, 40)).astype(np.float32)
+    w = rng.standard_normal((7, 40)).astype(np.float32)
+    wc, ws = oracle.int8_codes(w)
+    y, acc, xs, xc = oracle.w8a8_dense(x, wc, ws)
+    for i in range(5):
+        for j in range(7):
+            exact = sum(int(a) * int(b) for a, b in zip(xc[i], wc[j]))
+            assert acc[i, j] == exact
+    # a transposed weight is caught
+    bad = np.dot(xc.astype(np.float64), wc.astype(np.float64)[:, ::-1].T)
+    assert not np.array_equal(bad.astype(np.int32), acc)
+    # y is the rescaled accumulator
+    want = (acc.astype(np.float64) * xs.astype(np.float64)) * ws.reshape(1, -1).astype(np.float64)
+    assert np.allclose(y, want, rtol=1e-6, atol=1e-6)
+
+
+def test_dense_forward_matches_float64_math():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((9, 31)).astype(np.float32)
+    w = (rng.standard_normal((6, 31)) * 0.1).astype(np.float32)
+    b = rng.standard_normal(6).astype(np.float32)
+    layer = {"type": "dense", "weights": w, "bias": b, "activation": "linear"}
+    y, z = oracle.dense_forward(layer, x)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T + b
+    assert np.max(np.abs(z - exact)) < 1e-5
+    layer["activation"] = "relu"
+    y, _ = oracle.dense_forward(layer, x)
+    assert np.array_equal(y, np.where(z < 0, 0, z))
+
+
+def test_activation_closed_forms():
+    x = np.array([-3.0, -0.5, 0.0, 0.5, 3.0])
+    assert np.allclose(oracle.activate("sigmoid", x), 1 / (1 + np.exp(-x)))
+    assert oracle.activate("gelu", np.array([0.0]))[0] == 0.0
+    g = oracle.activate("gelu", np.array([10.0]))[0]
+    assert abs(g - 10.0) < 1e-12
+    assert np.allclose(oracle.activate("swish", x), x / (1 + np.exp(-x)))
+    assert np.allclose(oracle.activate("softplus", x), np.log1p(np.exp(x)))
+    sm = oracle.activate("softmax", np.array([[1.0, 2.0, 3.0]]))
+    assert abs(sm.sum() - 1) < 1e-12 and np.all(np.diff(sm[0]) > 0)
+    with pytest.raises(ValueError):
+        oracle.activate("nope", x)
+
+
+def _moe_layer(rng, d=6, h=10, e=4, k=2):
+    return {"type": "moe", "embed_dim": d, "num_experts": e, "top_k": k,
+            "hidden_dim": h, "activation": "gelu",
+            "W1": rng.standard_normal((e, h, d)) * 0.3, "b1": rng.standard_normal((e, h)) * 0.1,
+            "W2": rng.standard_normal((e, d, h)) * 0.3, "b2": rng.standard_normal((e, d)) * 0.1,
+            "Wr": rng.standard_normal((e, d)) * 0.5, "br": np.zeros(e)}
+
+
+def test_moe_matches_dense_mixture():
+    # test_enilnets.py:8331-8353: run every expert on every token and keep
+    # the top-k gates; must equal the routed computation in float64.
+    rng = np.random.default_rng(13)
+    layer = _moe_layer(rng)
+    x = rng.standard_normal((3, 5, 6))
+    got = oracle.moe_forward(x, layer)
+    flat = x.reshape(-1, 6)
+    logits = flat @ layer["Wr"].T + layer["br"]
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p = p / p.sum(axis=1, keepdims=True)
+    want = np.zeros_like(flat)
+    for t in range(flat.shape[0]):
+        top = np.argsort(-p[t])[:2]
+        for e in range(4):
+            h = oracle.activate("gelu", flat[t] @ layer["W1"][e].T + layer["b1"][e])
+            y = h @ layer["W2"][e].T + layer["b2"][e]
+            if e in top:
+                want[t] += p[t, e] * y
+    assert np.allclose(got.reshape(-1, 6), want, atol=1e-10, rtol=0)
