@@ -1,0 +1,345 @@
+#!/usr/bin/env python3
+"""Benchmark of Enilnets' quantized-inference hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-components] [--no-cpu]
+
+Headline (``value``): BASELINE.json configs[1], the 3-layer MLP
+784 -> 1024 -> 1024 -> 10 with per-output-channel int8 weights (He-normal
+fp32 init, biases ~N(0, 0.01)), ReLU hidden layers, batch 4096 of U(0, 1)
+activations.  One step is the three fused dequant-GEMMs of that batch on the
+fp32-accurate W8 path, inputs resident in HBM; the metric is the step's
+algorithmic TFLOP/s (2 * M * sum(N * K)).
+
+``components`` reports the BASELINE configs[2] kernels (8192 x 8192 weight):
+quantize / dequantize GB/s, the M=16 GEMV, the M=4096 W8 GEMM in both
+variants, per-token activation quantization and the W8A8 int8 GEMM at
+M=4096 and 8192^3.  Memory-bound kernels rotate over enough buffers to
+exceed the 256 MB MALL, so their bytes come from HBM.
+
+``roofline`` is the dominant kernel of the headline step (the largest MLP
+layer's W8 GEMM), timed with HIP events on the library stream.
+``cpu_baseline`` times the NumPy oracle (the reference's CPU path, restated)
+on the host for a bounded sample of the same step.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA
+INT8_PEAK_TOPS = 5000.0        # dense int8 MFMA
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-components", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of component names (debug)")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events recorded on the library stream."""
+
+    def __init__(self):
+        import ctypes
+        from enilnets_amd import _lib
+        self._lib, self._ct = _lib, ctypes
+        self.a, self.b = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.call("enq_event_create", ctypes.byref(self.a))
+        _lib.call("enq_event_create", ctypes.byref(self.b))
+
+    def time(self, fn, reps):
+        """Average milliseconds per call over ``reps`` back-to-back calls."""
+        self._lib.call("enq_synchronize")
+        self._lib.call("enq_event_record", self.a)
+        for i in range(reps):
+            fn(i)
+        self._lib.call("enq_event_record", self.b)
+        ms = self._ct.c_float()
+        self._lib.call("enq_event_elapsed_ms", self.a, self.b, self._ct.byref(ms))
+        return ms.value / reps
+
+
+def mlp_weights(rng):
+    """He-normal weights (n_out, n_in), biases N(0, 0.01)."""
+    dims = [(784, 1024), (1024, 1024), (1024, 10)]
+    layers = []
+    for n_in, n_out in dims:
+        w = rng.normal(0.0, np.sqrt(2.0 / n_in), (n_out, n_in)).astype(np.float32)
+        b = rng.normal(0.0, 0.01, n_out).astype(np.float32)
+        layers.append((w, b))
+    return layers
+
+
+def build_mlp(rng):
+    from enilnets_amd import quantize_weights
+    from enilnets_amd.nn import Model
+    m = Model()
+    acts = ["relu", "relu", "linear"]
+    for (w, b), act in zip(mlp_weights(rng), acts):
+        m.add_dense(w, b, act)
+    quantize_weights(m, bits=8, per_channel=True)
+    return m
+
+
+def cpu_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        info = [i for i in threadpool_info() if i.get("user_api") == "blas"]
+        if info:
+            return int(info[0]["num_threads"])
+    except Exception:
+        pass
+    return os.cpu_count() or 1
+
+
+def cpu_baseline(model, x, budget_s=12.0):
+    """The NumPy oracle's Dense chain (fake-quantized weights, fp32 sgemm) on
+    the host: median seconds per step over a bounded number of steps."""
+    import oracle
+    layers = model.layers
+    oracle.forward(layers, x[:256])          # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s and len(times) < 50:
+        t0 = time.perf_counter()
+        oracle.forward(layers, x)
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def headline(args, timer, rng):
+    from enilnets_amd.device import DeviceArray
+    from enilnets_amd.nn import int8_weights
+    from enilnets_amd.nn.dense import dense_w8
+    model = build_mlp(rng)
+    M = 4096
+    x = rng.uniform(0.0, 1.0, (M, 784)).astype(np.float32)
+    d_x = DeviceArray.from_numpy(x)
+    ws = [int8_weights(l, "weights") for l in model.layers]
+    bs = [DeviceArray.from_numpy(l["bias"]) for l in model.layers]
+    acts = [l["activation"] for l in model.layers]
+    outs = [DeviceArray((M, w.shape[0]), np.float32) for w in ws]
+
+    def step(_=0):
+        h = d_x
+        for w, b, a, o in zip(ws, bs, acts, outs):
+            h = dense_w8(h, w, b, a, variant="fp32", out=o)
+        return h
+
+    # correctness guard on a few rows against the oracle (float64 math)
+    y = step().numpy()
+    import oracle
+    ref = oracle.forward(model.layers, x[:64].astype(np.float64), dtype=np.float64)[-1]
+    rel = np.max(np.abs(y[:64] - ref)) / max(np.max(np.abs(ref)), 1e-30)
+    if not rel < 1e-3:
+        raise SystemExit(f"bench: MLP output differs from the oracle (rel {rel:.3e})")
+
+    flops = 2.0 * M * sum(w.shape[0] * w.shape[1] for w in ws)
+    for _ in range(args.warmup):
+        step()
+    ms = timer.time(step, args.steps)
+    # dominant kernel: the largest layer's GEMM, timed alone
+    big = int(np.argmax([w.shape[0] * w.shape[1] for w in ws]))
+    h_in = d_x if big == 0 else outs[big - 1]
+    w_big = ws[big]
+    reps = max(args.steps, 20)
+    k_ms = timer.time(lambda i: dense_w8(h_in, w_big, bs[big], acts[big], variant="fp32",
+                                         out=outs[big]), reps)
+    k_flops = 2.0 * M * w_big.shape[0] * w_big.shape[1]
+    return model, x, flops, ms, {"layer": big, "m": M, "n": w_big.shape[0],
+                                 "k": w_big.shape[1], "ms": k_ms, "flops": k_flops}
+
+
+def components(timer, rng, only):
+    """BASELINE configs[2] kernels."""
+    import ctypes
+    from enilnets_amd import _lib
+    from enilnets_amd.device import DeviceArray, null
+    from enilnets_amd.nn.dense import dense_w8, gemm_w8a8, quantize_rows_i8
+    from enilnets_amd.nn.weights import Int8Weights
+    N = K = 8192
+    out = {}
+    want = set(only.split(",")) if only else None
+
+    def on(name):
+        return want is None or name in want
+
+    copies = 5   # 5 x 268 MB fp32 or 5 x 67 MB int8 > 256 MB MALL
+    w_host = rng.normal(0.0, 0.02, (N, K)).astype(np.float32)
+    d_ws = [DeviceArray.from_numpy(w_host) for _ in range(copies)]
+    d_codes = [DeviceArray((N, K), np.int8) for _ in range(copies)]
+    d_scale = [DeviceArray((N,), np.float32) for _ in range(copies)]
+    d_zp = DeviceArray((N,), np.float32)
+    nk = N * K
+
+    if on("quantize"):
+        def q(i):
+            j = i % copies
+            _lib.call("enq_quantize_tensor", _lib.F32, d_ws[j].ptr, 1, N, K, 8, _lib.SYMMETRIC,
+                      null(), d_codes[j].ptr, d_scale[j].ptr, d_zp.ptr, null())
+        q(0)
+        ms = timer.time(q, 30)
+        nbytes = 4 * nk + nk + 4 * N
+        out["quantize_8192x8192_per_channel_int8"] = {
+            "ms": ms, "GB/s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            "bytes": nbytes}
+    else:
+        for j in range(copies):
+            _lib.call("enq_quantize_tensor", _lib.F32, d_ws[j].ptr, 1, N, K, 8, _lib.SYMMETRIC,
+                      null(), d_codes[j].ptr, d_scale[j].ptr, d_zp.ptr, null())
+
+    if on("fake_quantize"):
+        d_fake = [DeviceArray((N, K), np.float32) for _ in range(2)]
+
+        def fq(i):
+            j = i % copies
+            _lib.call("enq_quantize_tensor", _lib.F32, d_ws[j].ptr, 1, N, K, 8, _lib.SYMMETRIC,
+                      d_fake[i % 2].ptr, null(), d_scale[j].ptr, d_zp.ptr, null())
+        fq(0)
+        ms = timer.time(fq, 20)
+        nbytes = 8 * nk + 8 * N
+        out["quantize_tensor_fake_8192x8192"] = {
+            "ms": ms, "GB/s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            "bytes": nbytes}
+        del d_fake
+
+    if on("dequantize"):
+        def dq(i):
+            j = i % copies
+            _lib.call("enq_dequantize_i8", _lib.F32, d_codes[j].ptr, 1, N, K, d_scale[j].ptr,
+                      d_ws[j].ptr)
+        dq(0)
+        ms = timer.time(dq, 30)
+        nbytes = nk + 4 * N + 4 * nk
+        out["dequantize_8192x8192_int8"] = {
+            "ms": ms, "GB/s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            "bytes": nbytes}
+
+    wq = [Int8Weights(d_codes[j], d_scale[j], (N, K), 8, True, None, None) for j in range(copies)]
+    del d_ws
+
+    if on("gemv"):
+        M = 16
+        x = DeviceArray.from_numpy(rng.standard_normal((M, K)).astype(np.float32))
+        y = DeviceArray((M, N), np.float32)
+        f = lambda i: dense_w8(x, wq[i % copies], None, "linear", out=y)
+        f(0)
+        ms = timer.time(f, 50)
+        nbytes = nk + 4 * M * K + 4 * M * N + 8 * N
+        out["gemv_w8_fp32_m16"] = {
+            "ms": ms, "GB/s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            "TFLOP/s": 2 * M * nk / ms / 1e9, "bytes": nbytes}
+
+    M = 4096
+    x4 = DeviceArray.from_numpy(rng.standard_normal((M, K)).astype(np.float32))
+    y4 = DeviceArray((M, N), np.float32)
+    flops = 2.0 * M * nk
+    for variant in ("fp32", "bf16"):
+        if on("gemm_" + variant):
+            f = lambda i, v=variant: dense_w8(x4, wq[i % 2], None, "linear", variant=v, out=y4)
+            f(0)
+            ms = timer.time(f, 10)
+            tf = flops / ms / 1e9
+            out[f"gemm_w8_{variant}_m4096"] = {
+                "ms": ms, "TFLOP/s": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS}
+
+    if on("act_quant"):
+        xc, xs = quantize_rows_i8(x4)
+        f = lambda i: _lib.call("enq_quantize_rows_i8", x4.ptr, M, K, xc.ptr, xs.ptr)
+        ms = timer.time(f, 30)
+        nbytes = 5 * M * K + 4 * M
+        out["per_token_quantize_m4096"] = {
+            "ms": ms, "GB/s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            "bytes": nbytes}
+
+    if on("w8a8"):
+        xc, xs = quantize_rows_i8(x4)
+        f = lambda i: gemm_w8a8(xc, xs, wq[i % 2], out=y4)
+        f(0)
+        ms = timer.time(f, 10)
+        tops = flops / ms / 1e9
+        out["gemm_w8a8_m4096"] = {"ms": ms, "TOP/s": tops, "frac_int8_peak": tops / INT8_PEAK_TOPS}
+        del xc, xs
+        xsq = DeviceArray.from_numpy(rng.integers(-127, 128, (8192, K), dtype=np.int8))
+        ssq = DeviceArray.from_numpy(np.full(8192, 0.01, np.float32))
+        ysq = DeviceArray((8192, N), np.float32)
+        f = lambda i: gemm_w8a8(xsq, ssq, wq[i % 2], out=ysq)
+        f(0)
+        ms = timer.time(f, 10)
+        tops = 2.0 * 8192 * nk / ms / 1e9
+        out["gemm_w8a8_8192cubed"] = {"ms": ms, "TOP/s": tops,
+                                      "frac_int8_peak": tops / INT8_PEAK_TOPS}
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build measures the "
+              "one-GPU path; sharding across GPUs is described in DESIGN.md, not run.",
+              file=sys.stderr)
+        return 2
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from enilnets_amd import _lib
+    _lib.lib()
+    info = _lib.device_info()
+    print(f"[bench] device {info.name.decode()} {info.arch.decode()} CUs={info.compute_units}",
+          file=sys.stderr, flush=True)
+    rng = np.random.default_rng(0)
+    timer = Timer()
+    model, x, flops, ms, dom = headline(args, timer, rng)
+    print(f"[bench] MLP step {ms:.4f} ms", file=sys.stderr, flush=True)
+    value = flops / ms / 1e9
+    dom_tf = dom["flops"] / dom["ms"] / 1e9
+    result = {
+        "metric": "W8 Dense GEMM TFLOP/s (BASELINE configs[1] MLP step, fp32-accurate W8)",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights x fp32 activations (bf16 hi+lo MFMA, fp32 accumulate)",
+        "data": "synthetic (seeded He-normal weights, U(0,1) activations)",
+        "config": {"workload": "configs[1]: MLP 784-1024-1024-10, ReLU, batch 4096, "
+                               "per-output-channel int8 weights",
+                   "global_batch": 4096, "layers": 3, "variant": "fp32",
+                   "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "kernel": "w8_gemm_kernel",
+                     "shape": [dom["m"], dom["n"], dom["k"]],
+                     "achieved": round(dom_tf, 3), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(dom_tf / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None,
+                     "note": "algorithmic 2*M*N*K over the measured time of the layer's "
+                             "dense call; the fp32-accurate path issues two bf16 MFMA "
+                             "passes (hi, lo) per product"},
+    }
+    if not args.no_components:
+        result["components"] = components(timer, rng, args.only)
+    if not args.no_cpu:
+        sec, n = cpu_baseline(model, x)
+        result["cpu_baseline"] = {
+            "value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s", "cores": cpu_threads(),
+            "kind": "port",
+            "sample": f"NumPy oracle Dense chain (fake-quantized fp32 weights, BLAS sgemm), "
+                      f"full batch 4096, median of {n} steps",
+            "ms_per_step": round(sec * 1e3, 3)}
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -53,6 +53,25 @@ __device__ __forceinline__ float activate(float x, const Epilogue& e) {
   }
 }
 
+// Calls body(f) with f the activation as a callable, so the common
+// activations compile into straight-line epilogues instead of a switch per
+// element.
+template <class Body>
+__device__ __forceinline__ void with_activation(const Epilogue& ep, Body&& body) {
+  switch (ep.activation) {
+    case ENQ_ACT_LINEAR:
+    case ENQ_ACT_SOFTMAX:
+      body([](float x) { return x; });
+      break;
+    case ENQ_ACT_RELU:
+      body([](float x) { return x < 0.0f ? 0.0f : x; });
+      break;
+    default:
+      body([ep](float x) { return activate(x, ep); });
+      break;
+  }
+}
+
 // Row-wise softmax in place over an (m, n) fp32 matrix (activations.py:38-40).
 void softmax_rows(float* y, int64_t m, int64_t n);
 

@@ -1,0 +1,76 @@
+// Tile scheduling and LDS staging helpers shared by the GEMM kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace enq {
+
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+// L2.  Logical tiles are assigned so that each XCD owns one contiguous run
+// of tiles, ordered in groups of `group_m` tile rows: the tiles that run at
+// the same time on one XCD then share A row panels and B column panels in
+// that XCD's L2.  The mapping is a bijection for any grid size.
+__device__ __forceinline__ void xcd_tile(int bid, int tiles_m, int tiles_n, int group_m,
+                                         int& tm, int& tn) {
+  constexpr int kXcds = 8;
+  const int total = tiles_m * tiles_n;
+  const int per = total / kXcds, rem = total % kXcds;
+  const int xcd = bid % kXcds, local = bid / kXcds;
+  const int t = xcd * per + (xcd < rem ? xcd : rem) + local;
+  const int group = group_m * tiles_n;
+  const int first_m = (t / group) * group_m;
+  const int rows = tiles_m - first_m < group_m ? tiles_m - first_m : group_m;
+  const int in_group = t % group;
+  tm = first_m + in_group % rows;
+  tn = in_group / rows;
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at "no wait").
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+}
+
+// s_waitcnt with only the LDS/scalar counter constrained to <= N.
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (N << 8) | (3 << 14));
+}
+
+// Keeps the machine scheduler from moving any instruction across this point.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Workgroup barrier that neither waits for outstanding loads nor lets the
+// compiler move memory operations across it.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 16 bytes from global memory straight into LDS (gfx950 global_load_lds_dwordx4).
+// LDS destination of lane l is lds_base + 16 * l: one instruction fills 1 KiB.
+__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(
+      (__attribute__((address_space(1))) void*)(const_cast<void*>(src)),
+      (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
+}
+
+// XOR swizzle of the four 16-byte chunks of a 64-byte LDS row: conflict-free
+// ds_read_b128 when lanes 0..31 read 32 consecutive rows at one chunk.
+__device__ __forceinline__ int swz64(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+
+// Zero bytes (static storage is zero-initialised): the DMA source for chunks
+// past the end of K.  One copy per translation unit.
+static __device__ __align__(16) int4 g_zero16[4];
+
+}  // namespace enq
