@@ -126,13 +126,27 @@ struct alignas(sizeof(T) * V) Vec {
   T v[V];
 };
 
+// Streaming (non-temporal) vector accesses: every tensor here is touched
+// once, so the loads and stores bypass cache allocation.
+template <class T, int V>
+struct NativeVec {
+  typedef T type __attribute__((ext_vector_type(V)));
+};
+template <class T>
+struct NativeVec<T, 1> {
+  typedef T type;
+};
+
 template <class T, int V>
 __device__ __forceinline__ Vec<T, V> load_vec(const T* p) {
-  return *reinterpret_cast<const Vec<T, V>*>(p);
+  typedef typename NativeVec<T, V>::type N;
+  N n = __builtin_nontemporal_load(reinterpret_cast<const N*>(p));
+  return __builtin_bit_cast(Vec<T, V>, n);
 }
 template <class T, int V>
 __device__ __forceinline__ void store_vec(T* p, const Vec<T, V>& v) {
-  *reinterpret_cast<Vec<T, V>*>(p) = v;
+  typedef typename NativeVec<T, V>::type N;
+  __builtin_nontemporal_store(__builtin_bit_cast(N, v), reinterpret_cast<N*>(p));
 }
 
 template <int V>
@@ -140,10 +154,10 @@ __device__ __forceinline__ void store_codes(int8_t* p, const int8_t (&c)[V]) {
   if constexpr (V == 4) {
     uint32_t packed = uint32_t(uint8_t(c[0])) | (uint32_t(uint8_t(c[1])) << 8) |
                       (uint32_t(uint8_t(c[2])) << 16) | (uint32_t(uint8_t(c[3])) << 24);
-    *reinterpret_cast<uint32_t*>(p) = packed;
+    __builtin_nontemporal_store(packed, reinterpret_cast<uint32_t*>(p));
   } else if constexpr (V == 2) {
     uint16_t packed = uint16_t(uint8_t(c[0])) | uint16_t(uint16_t(uint8_t(c[1])) << 8);
-    *reinterpret_cast<uint16_t*>(p) = packed;
+    __builtin_nontemporal_store(packed, reinterpret_cast<uint16_t*>(p));
   } else {
     p[0] = c[0];
   }
@@ -174,8 +188,30 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv& f) {
 // Per-row fused quantize_tensor: one row group (TPR threads) per row, the row
 // held in registers, so HBM is read once.  Used for per-channel quantization
 // along axis 0 (outer == 1) and for int8 per-row (per-token) codes.
+//
+// SYM: the symmetric scheme only needs max |x| (one fmax per element plus a
+// NaN flag); asymmetric tracks min and max.  OUT is a bitmask of the outputs
+// (kOutFake, kOutCodes, kOutErr) so unused ones cost neither instructions
+// nor registers.  All blocks walk their rows in the same chunk order, which
+// keeps HBM traffic in lockstep (measured: rotating the order per row halves
+// the bandwidth).
 // ---------------------------------------------------------------------------
-template <class T, int TPR, int CHUNKS, int V>
+constexpr int kOutFake = 1, kOutCodes = 2, kOutErr = 4;
+
+template <class T>
+__device__ __forceinline__ T fmax_t(T a, T b);
+template <>
+__device__ __forceinline__ float fmax_t<float>(float a, float b) { return __builtin_fmaxf(a, b); }
+template <>
+__device__ __forceinline__ double fmax_t<double>(double a, double b) { return __builtin_fmax(a, b); }
+template <class T>
+__device__ __forceinline__ T fmin_t(T a, T b);
+template <>
+__device__ __forceinline__ float fmin_t<float>(float a, float b) { return __builtin_fminf(a, b); }
+template <>
+__device__ __forceinline__ double fmin_t<double>(double a, double b) { return __builtin_fmin(a, b); }
+
+template <class T, int TPR, int CHUNKS, int V, bool SYM, int OUT>
 __global__ __launch_bounds__(TPR < kBlock ? kBlock : TPR) void rows_quant_kernel(
     const T* __restrict__ w, int64_t rows, int64_t cols, QParams p,
     T* __restrict__ out_fake, int8_t* __restrict__ out_codes,
@@ -183,8 +219,8 @@ __global__ __launch_bounds__(TPR < kBlock ? kBlock : TPR) void rows_quant_kernel
   constexpr int kThreads = TPR < kBlock ? kBlock : TPR;
   constexpr int kRowsPerBlock = kThreads / TPR;
   constexpr int kWavesPerRow = TPR / 64;
-  __shared__ T s_lo[kThreads / 64];
-  __shared__ T s_hi[kThreads / 64];
+  __shared__ T s_a[kThreads / 64];
+  __shared__ T s_b[kThreads / 64];
   __shared__ int s_nan[kThreads / 64];
   __shared__ double s_err[kThreads / 64];
 
@@ -194,35 +230,70 @@ __global__ __launch_bounds__(TPR < kBlock ? kBlock : TPR) void rows_quant_kernel
   const T* src = w + row * cols;
 
   T vals[CHUNKS][V];
-  Range<T> r;
-  r.init();
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const int64_t idx = (int64_t(c) * TPR + t) * V;
     if (active && idx < cols) {
       Vec<T, V> v = load_vec<T, V>(src + idx);
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        vals[c][e] = v.v[e];
-        r.add(v.v[e]);
+      for (int e = 0; e < V; ++e) vals[c][e] = v.v[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) vals[c][e] = T(0);
+    }
+  }
+  // a: max |x| (SYM) or min x; b: max x (asymmetric only).  Padding zeros do
+  // not change max |x|; for min / max they are excluded below.
+  T a = SYM ? T(0) : pos_inf<T>(), b = -pos_inf<T>();
+  int nan = 0;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int64_t idx = (int64_t(c) * TPR + t) * V;
+    const bool live = SYM || (active && idx < cols);
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const T x = vals[c][e];
+      nan |= (x != x);
+      if (SYM) {
+        a = fmax_t(a, x < T(0) ? -x : x);
+      } else if (live) {
+        a = fmin_t(a, x);
+        b = fmax_t(b, x);
       }
     }
   }
-  wave_reduce(r);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    a = SYM ? fmax_t(a, __shfl_xor(a, m, 64)) : fmin_t(a, __shfl_xor(a, m, 64));
+    if (!SYM) b = fmax_t(b, __shfl_xor(b, m, 64));
+    nan |= __shfl_xor(nan, m, 64);
+  }
   if constexpr (kWavesPerRow > 1) {
     const int wave = threadIdx.x / 64;
     if ((threadIdx.x & 63) == 0) {
-      s_lo[wave] = r.lo;
-      s_hi[wave] = r.hi;
-      s_nan[wave] = r.nan;
+      s_a[wave] = a;
+      if (!SYM) s_b[wave] = b;
+      s_nan[wave] = nan;
     }
     __syncthreads();
-    r.init();
+    const int first = (threadIdx.x / TPR) * kWavesPerRow;
+    a = s_a[first];
+    if (!SYM) b = s_b[first];
+    nan = s_nan[first];
 #pragma unroll
-    for (int i = 0; i < kWavesPerRow; ++i) r.merge(s_lo[i], s_hi[i], s_nan[i]);
+    for (int i = 1; i < kWavesPerRow; ++i) {
+      a = SYM ? fmax_t(a, s_a[first + i]) : fmin_t(a, s_a[first + i]);
+      if (!SYM) b = fmax_t(b, s_b[first + i]);
+      nan |= s_nan[first + i];
+    }
   }
   T scale, zp;
-  scale_from_range(r.low(), r.high(), p, scale, zp);
+  if (SYM) {
+    // compute_scale with low = -a, high = a gives max(|low|, |high|) = a
+    scale_from_range(nan ? nan_value<T>() : -a, nan ? nan_value<T>() : a, p, scale, zp);
+  } else {
+    scale_from_range(nan ? nan_value<T>() : a, nan ? nan_value<T>() : b, p, scale, zp);
+  }
   if (active && t == 0) {
     scale_out[row] = scale;
     zp_out[row] = zp;
@@ -238,26 +309,27 @@ __global__ __launch_bounds__(TPR < kBlock ? kBlock : TPR) void rows_quant_kernel
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         T q = quantize_one(vals[c][e], scale, zp, qmin, qmax);
-        f.v[e] = dequantize_one(q, scale, zp);
-        codes[e] = code_to_i8(q);
-        if (err_rows) {
+        if (OUT & (kOutFake | kOutErr)) f.v[e] = dequantize_one(q, scale, zp);
+        if (OUT & kOutCodes) codes[e] = code_to_i8(q);
+        if (OUT & kOutErr) {
           T d = f.v[e] - vals[c][e];
           err += double(d < 0 ? -d : d);
         }
       }
-      if (out_fake) store_vec<T, V>(out_fake + row * cols + idx, f);
-      if (out_codes) store_codes<V>(out_codes + row * cols + idx, codes);
+      if (OUT & kOutFake) store_vec<T, V>(out_fake + row * cols + idx, f);
+      if (OUT & kOutCodes) store_codes<V>(out_codes + row * cols + idx, codes);
     }
   }
-  if (err_rows) {
+  if (OUT & kOutErr) {
     err = wave_sum(err);
     if constexpr (kWavesPerRow > 1) {
       const int wave = threadIdx.x / 64;
       if ((threadIdx.x & 63) == 0) s_err[wave] = err;
       __syncthreads();
+      const int first = (threadIdx.x / TPR) * kWavesPerRow;
       err = 0.0;
 #pragma unroll
-      for (int i = 0; i < kWavesPerRow; ++i) err += s_err[i];
+      for (int i = 0; i < kWavesPerRow; ++i) err += s_err[first + i];
     }
     if (active && t == 0) err_rows[row] = err;
   }
@@ -578,6 +650,47 @@ __global__ __launch_bounds__(kBlock) void elementwise_kernel(
   }
 }
 
+// int8 codes -> T with a per-channel scale.  A lane handles 4 consecutive
+// codes per step (one 32-bit load), so every wave store is one contiguous
+// 1 KiB run (fp32) and every wave load a contiguous 256 B run; four steps
+// are in flight per iteration.  Requires n % 4 == 0, inner % 4 == 0 (a step
+// never spans channels), 4-byte aligned codes and 16-byte aligned output.
+template <class T>
+__global__ __launch_bounds__(kBlock) void dequant_i8_kernel(const int8_t* __restrict__ codes,
+                                                            int64_t n, ChannelMap map,
+                                                            const T* __restrict__ scale,
+                                                            T* __restrict__ out) {
+  constexpr int kUnroll = 4;
+  const uint32_t* c32 = reinterpret_cast<const uint32_t*>(codes);
+  const int64_t units = n / 4;
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  int64_t u = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  for (; u + (kUnroll - 1) * stride < units; u += kUnroll * stride) {
+    uint32_t raw[kUnroll];
+    T s[kUnroll];
+#pragma unroll
+    for (int r = 0; r < kUnroll; ++r) {
+      raw[r] = __builtin_nontemporal_load(c32 + u + r * stride);
+      s[r] = scale[channel_of((u + r * stride) * 4, map)];
+    }
+#pragma unroll
+    for (int r = 0; r < kUnroll; ++r) {
+      Vec<T, 4> v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v.v[e] = T(int8_t((raw[r] >> (8 * e)) & 0xff)) * s[r];
+      store_vec<T, 4>(out + (u + r * stride) * 4, v);
+    }
+  }
+  for (; u < units; u += stride) {
+    const uint32_t raw = __builtin_nontemporal_load(c32 + u);
+    const T s = scale[channel_of(u * 4, map)];
+    Vec<T, 4> v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v.v[e] = T(int8_t((raw >> (8 * e)) & 0xff)) * s;
+    store_vec<T, 4>(out + u * 4, v);
+  }
+}
+
 // Deterministic sum of `n` doubles into out[0] (one block).
 __global__ __launch_bounds__(kBlock) void sum_doubles_kernel(const double* __restrict__ in,
                                                              int64_t n, double* __restrict__ out) {
@@ -712,9 +825,9 @@ ChannelMap make_map(int64_t n, int64_t channels, int64_t inner) {
   return m;
 }
 
-int grid_for(int64_t work_items) {
+int grid_for(int64_t work_items, int per_cu = 8) {
   int64_t blocks = ceil_div(work_items, kBlock);
-  int64_t cap = int64_t(device_cu_count() > 0 ? device_cu_count() : 256) * 8;
+  int64_t cap = int64_t(device_cu_count() > 0 ? device_cu_count() : 256) * per_cu;
   if (blocks > cap) blocks = cap;
   return int(blocks < 1 ? 1 : blocks);
 }
@@ -806,9 +919,10 @@ void range_stats(const T* x, int64_t outer, int64_t channels, int64_t inner, QPa
   check_launch("finish_range_kernel");
 }
 
-// Row-kernel configurations: (threads per row, 16-byte chunks per thread).
-template <class T, int V>
-bool launch_rows(const T* w, int64_t rows, int64_t cols, QParams p, T* fake, int8_t* codes,
+// Row-kernel configurations: (threads per row, 16-byte chunks per thread),
+// the smallest that holds the row in registers.
+template <class T, int V, bool SYM, int OUT>
+void launch_rows(const T* w, int64_t rows, int64_t cols, QParams p, T* fake, int8_t* codes,
                  T* scale, T* zp, double* err_rows) {
   auto go = [&](auto kernel, int tpr) {
     const int threads = tpr < kBlock ? kBlock : tpr;
@@ -818,19 +932,38 @@ bool launch_rows(const T* w, int64_t rows, int64_t cols, QParams p, T* fake, int
     kernel<<<unsigned(grid), threads, 0, stream()>>>(w, rows, cols, p, fake, codes, scale, zp,
                                                      err_rows);
     check_launch("rows_quant_kernel");
-    return true;
   };
-  if (cols <= 64 * 4 * V) return go(rows_quant_kernel<T, 64, 4, V>, 64);
-  if (cols <= 256 * 4 * V) return go(rows_quant_kernel<T, 256, 4, V>, 256);
-  if (cols <= 256 * 8 * V) return go(rows_quant_kernel<T, 256, 8, V>, 256);
-  if (cols <= 512 * 8 * V) return go(rows_quant_kernel<T, 512, 8, V>, 512);
-  if (cols <= 1024 * 8 * V) return go(rows_quant_kernel<T, 1024, 8, V>, 1024);
+  if (cols <= 64 * 4 * V) return go(rows_quant_kernel<T, 64, 4, V, SYM, OUT>, 64);
+  if (cols <= 256 * 4 * V) return go(rows_quant_kernel<T, 256, 4, V, SYM, OUT>, 256);
+  if (cols <= 512 * 4 * V) return go(rows_quant_kernel<T, 512, 4, V, SYM, OUT>, 512);
+  if (cols <= 1024 * 4 * V) return go(rows_quant_kernel<T, 1024, 4, V, SYM, OUT>, 1024);
+  if (cols <= 1024 * 8 * V) return go(rows_quant_kernel<T, 1024, 8, V, SYM, OUT>, 1024);
   ENQ_REQUIRE(rows <= 0x7fffffff, "too many rows");
   rows_quant_stream_kernel<T, V><<<unsigned(rows), 1024, 0, stream()>>>(w, rows, cols, p, fake,
                                                                          codes, scale, zp,
                                                                          err_rows);
   check_launch("rows_quant_stream_kernel");
-  return true;
+}
+
+template <class T, int V>
+void launch_rows_any(const T* w, int64_t rows, int64_t cols, QParams p, T* fake, int8_t* codes,
+                     T* scale, T* zp, double* err_rows) {
+  const int out = (fake ? kOutFake : 0) | (codes ? kOutCodes : 0) | (err_rows ? kOutErr : 0);
+  const bool sym = p.scheme == ENQ_SYMMETRIC;
+#define ENQ_ROWS_CASE(SYMV, OUTV)                                                            \
+  if (sym == (SYMV) && out == (OUTV))                                                        \
+    return launch_rows<T, V, (SYMV), (OUTV)>(w, rows, cols, p, fake, codes, scale, zp, err_rows);
+  ENQ_ROWS_CASE(true, kOutCodes)
+  ENQ_ROWS_CASE(true, kOutFake)
+  ENQ_ROWS_CASE(true, kOutFake | kOutErr)
+  ENQ_ROWS_CASE(true, kOutFake | kOutCodes | kOutErr)
+  ENQ_ROWS_CASE(true, kOutFake | kOutCodes)
+  ENQ_ROWS_CASE(false, kOutFake)
+  ENQ_ROWS_CASE(false, kOutFake | kOutErr)
+#undef ENQ_ROWS_CASE
+  // any other combination: the general kernel computes every output it is given
+  return launch_rows<T, V, false, kOutFake | kOutCodes | kOutErr>(w, rows, cols, p, fake, codes,
+                                                                 scale, zp, err_rows);
 }
 
 template <class T>
@@ -840,9 +973,9 @@ void rows_quantize(const T* w, int64_t rows, int64_t cols, QParams p, T* fake, i
   const bool vec_ok = (cols % V) == 0 && aligned(w, 16) && (fake == nullptr || aligned(fake, 16)) &&
                       (codes == nullptr || aligned(codes, V));
   if (vec_ok)
-    launch_rows<T, V>(w, rows, cols, p, fake, codes, scale, zp, err_rows);
+    launch_rows_any<T, V>(w, rows, cols, p, fake, codes, scale, zp, err_rows);
   else
-    launch_rows<T, 1>(w, rows, cols, p, fake, codes, scale, zp, err_rows);
+    launch_rows_any<T, 1>(w, rows, cols, p, fake, codes, scale, zp, err_rows);
 }
 
 // Whether the one-pass row kernel (row held in registers) suits the shape:
@@ -976,8 +1109,15 @@ static int elementwise_entry(Op op, int dtype, const void* x, int64_t outer, int
                                            grid);
           break;
         case Op::kDequantI8:
-          launch_elementwise<T, Op::kDequantI8>(x, n, channels, inner, s, nullptr, p, o, nullptr,
-                                                nullptr, grid);
+          if (n % 4 == 0 && inner % 4 == 0 && aligned(x, 4) && aligned(o, 16)) {
+            const int g = grid_for(n / 16, 8);
+            dequant_i8_kernel<T><<<g, kBlock, 0, stream()>>>(
+                static_cast<const int8_t*>(x), n, make_map(n, channels, inner), s, o);
+            check_launch("dequant_i8_kernel");
+          } else {
+            launch_elementwise<T, Op::kDequantI8>(x, n, channels, inner, s, nullptr, p, o,
+                                                  nullptr, nullptr, grid);
+          }
           break;
         default:
           fail(ENQ_ERR_INVALID, "bad op");

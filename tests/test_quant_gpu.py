@@ -237,3 +237,25 @@ def test_dequantize_i8(gpu):
     _lib.call("enq_dequantize_i8", _lib.F32, d_c.ptr, 1, 33, 70, d_s.ptr, out.ptr)
     want = oracle.dequantize(codes.astype(np.float32), scale, np.zeros_like(scale))
     assert np.array_equal(out.numpy(), want)   # == semantics: int8 0 gives +0.0
+
+
+@pytest.mark.parametrize("shape", [(64, 48), (1024, 784), (10, 1024), (300, 2000), (33, 9000)])
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_quantize_weights_keeps_device_int8_codes(gpu, shape, per_channel):
+    # the codes cached for the integer kernels equal the oracle's codes
+    from enilnets_amd.nn.weights import int8_weights
+    rng = np.random.default_rng(shape[0])
+
+    class M:
+        pass
+    m = M()
+    w = (rng.standard_normal(shape) * 0.05).astype(np.float32)
+    m.layers = [{"type": "dense", "weights": w, "bias": np.zeros(shape[0], np.float32),
+                 "activation": "linear"}]
+    ea.quantize_weights(m, bits=8, per_channel=per_channel)
+    wq = int8_weights(m.layers[0], "weights")
+    want_codes, want_scale = oracle.int8_codes(w, per_channel=per_channel)
+    assert np.array_equal(wq.codes.numpy(), want_codes)
+    rows = np.broadcast_to(np.asarray(want_scale, np.float32).reshape(-1), (shape[0],)) \
+        if per_channel else np.full(shape[0], np.float32(want_scale))
+    assert np.array_equal(wq.scale.numpy(), rows)
