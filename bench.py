@@ -35,6 +35,21 @@ BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA
 INT8_PEAK_TOPS = 5000.0        # dense int8 MFMA
 
 
+def measured_traffic(name, shape):
+    """HBM bytes per launch of a kernel, from the rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes summarised in profiles/traffic.json (None if that
+    kernel and shape were not profiled)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+    if not entry or list(entry.get("shape", [])) != list(shape):
+        return None
+    return entry.get("bytes_per_launch")
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -173,6 +188,17 @@ def components(timer, rng, only):
 
     def on(name):
         return want is None or name in want
+
+    # known-size copy: rocprofv3's FETCH_SIZE / WRITE_SIZE of this blit
+    # calibrate the traffic counters of the kernels below
+    if on("calibration_copy"):
+        import ctypes
+        nbytes = 256 << 20
+        src_c, dst_c = DeviceArray((nbytes,), np.uint8), DeviceArray((nbytes,), np.uint8)
+        f = lambda i: _lib.call("enq_copy_on_device", dst_c.ptr, src_c.ptr, ctypes.c_size_t(nbytes))
+        ms = timer.time(f, 5)
+        out["calibration_copy_256MiB"] = {"ms": ms, "GB/s": 2 * nbytes / ms / 1e6, "bytes": nbytes}
+        del src_c, dst_c
 
     copies = 5   # 5 x 268 MB fp32 or 5 x 67 MB int8 > 256 MB MALL
     w_host = rng.normal(0.0, 0.02, (N, K)).astype(np.float32)
@@ -322,7 +348,7 @@ def main():
                      "shape": [dom["m"], dom["n"], dom["k"]],
                      "achieved": round(dom_tf, 3), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(dom_tf / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic("mlp_layer_gemm", [dom["m"], dom["n"], dom["k"]]),
                      "note": "algorithmic 2*M*N*K over the measured time of the layer's "
                              "dense call; the fp32-accurate path issues two bf16 MFMA "
                              "passes (hi, lo) per product"},

@@ -10,17 +10,21 @@
 //
 // Kernels
 //   split_planes_kernel  x (m, k) fp32 -> P bf16 planes (mp, kp), zero padded
-//   gemv_w8_kernel       m <= 64: split-K, W streamed once with 128-bit loads,
-//                        16x16x32 bf16 MFMA, partial sums per K-split
+//   gemv_w8_kernel       m <= 64, or n <= 32 (grid z over 16-row blocks):
+//                        split-K, W streamed with 128-bit loads, 16x16x32
+//                        bf16 MFMA, partial sums per K-split
 //   gemv_finish_kernel   sums the K-split partials, scale, bias, activation
-//   w8_gemm_kernel       m > 64: LDS-tiled, double-buffered 32x32x16 bf16
-//                        MFMA GEMM; int8 tiles are expanded to bf16 while
-//                        being staged into LDS; fused epilogue
+//   w8_ring_kernel       m > 64: direct-to-LDS multi-stage ring, int8 tiles
+//                        expanded to bf16 in registers, fused epilogue
+//   w8_gemm_kernel       the same GEMM with register staging, for K not a
+//                        multiple of 16 or unaligned codes
 #include <algorithm>
+#include <cstdlib>
 
 #include "common.hpp"
 #include "epilogue.hpp"
 #include "mfma.hpp"
+#include "tiling.hpp"
 
 namespace enq {
 namespace {
@@ -92,6 +96,9 @@ __device__ __forceinline__ int4 load_codes16(const int8_t* __restrict__ w, int64
 // ---------------------------------------------------------------------------
 constexpr int kGemvWaves = 8;
 constexpr int kGemvChunk = 128;
+// outputs this narrow go through the GEMV even for many rows: a GEMM tile
+// grid over them has too few workgroups to stream the activations
+constexpr int64_t kSkinnyN = 32;
 
 template <int MB, int PLANES, int CHUNKS, int KMODE>
 __global__ __launch_bounds__(512) void gemv_w8_kernel(
@@ -104,6 +111,9 @@ __global__ __launch_bounds__(512) void gemv_w8_kernel(
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int64_t k_wave0 = (int64_t(blockIdx.y) * kGemvWaves + wave) * chunks_per_wave * kGemvChunk;
+  // blockIdx.z selects a block of MB x 16 activation rows (tall-skinny use)
+  const int64_t row0 = int64_t(blockIdx.z) * (MB * 16);
+  xa += row0 * kp;
 
   // activation fragments for this wave's K range
   bf16x8 xf[CHUNKS][MB][PLANES][4];
@@ -122,7 +132,7 @@ __global__ __launch_bounds__(512) void gemv_w8_kernel(
       }
   }
 
-  const int64_t mp = MB * 16;
+  const int64_t mp = int64_t(gridDim.z) * (MB * 16);
   for (int cb = 0; cb < col_blocks_per_group; ++cb) {
     const int64_t n0 = (int64_t(blockIdx.x) * col_blocks_per_group + cb) * 16;
     if (n0 >= n) break;
@@ -166,7 +176,7 @@ __global__ __launch_bounds__(512) void gemv_w8_kernel(
       float s = 0.f;
 #pragma unroll
       for (int v = 0; v < kGemvWaves; ++v) s += red[v][mm][nn];
-      if (n0 + nn < n) part[(int64_t(blockIdx.y) * mp + mm) * n + n0 + nn] = s;
+      if (n0 + nn < n) part[(int64_t(blockIdx.y) * mp + row0 + mm) * n + n0 + nn] = s;
     }
     __syncthreads();
   }
@@ -201,7 +211,7 @@ template <int BM, int BN, int WM, int WN, int PLANES, int KMODE>
 __global__ __launch_bounds__(WM * WN * 64) void w8_gemm_kernel(
     const uint16_t* __restrict__ xa, int64_t plane_stride, int64_t kp,
     const int8_t* __restrict__ w, int64_t ldw, const float* __restrict__ scale,
-    const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_n,
+    const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n,
     Epilogue ep, float* __restrict__ y, float* __restrict__ z) {
   constexpr int NT = WM * WN * 64;
   constexpr int TM = BM / WM, TN = BN / WN;
@@ -221,9 +231,10 @@ __global__ __launch_bounds__(WM * WN * 64) void w8_gemm_kernel(
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  const int tile = blockIdx.x;
-  const int64_t m0 = int64_t(tile / tiles_n) * BM;
-  const int64_t n0 = int64_t(tile % tiles_n) * BN;
+  int tm, tn;
+  xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
+  const int64_t m0 = int64_t(tm) * BM;
+  const int64_t n0 = int64_t(tn) * BN;
 
   // global -> register staging
   int4 a_reg[A_PER_T];
@@ -338,6 +349,255 @@ __global__ __launch_bounds__(WM * WN * 64) void w8_gemm_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Ring W8 GEMM: activations as bf16 planes and int8 weight codes both stream
+// into an LDS ring through direct-to-LDS loads (global_load_lds_dwordx4),
+// STAGES - 1 stages in flight.  Per stage (32 columns of K):
+//   A: PLANES x BM rows of 64 bytes (32 bf16), chunks XOR-swizzled (swz64);
+//   B: BN rows of 32 bytes (32 codes), 16-byte halves swapped on bit 3 of the
+//      row, so 16 consecutive rows read at one half hit distinct banks.
+// Within a stage lane group g = l / 32 owns k in [16 g, 16 g + 16): the two
+// 32x32x16 MFMA steps take k 16 g + [0, 8) and 16 g + [8, 16), so one 128-bit
+// read gives a lane its 16 codes for the stage (expanded to bf16 in
+// registers), and A fragments are chunks 2 g and 2 g + 1 of the row.  The
+// schedule is the same software pipeline as the W8A8 ring kernel.
+// ---------------------------------------------------------------------------
+template <int BM_, int BN_, int WM_, int WN_, int PLANES_, int STAGES_>
+struct RingCfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, PLANES = PLANES_;
+  static constexpr int STAGES = STAGES_, BK = 32;
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  static constexpr int A_BYTES = PLANES * BM * 64;   // bf16 rows of 64 bytes
+  static constexpr int B_BYTES = BN * 32;            // code rows of 32 bytes
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int A_BLOCKS = A_BYTES / 1024, B_BLOCKS = B_BYTES / 1024;
+  static constexpr int BLOCKS = A_BLOCKS + B_BLOCKS;
+  // every wave issues the same number of 1 KiB blocks (vmcnt accounting);
+  // waves past the last block repeat it, rewriting identical bytes
+  static constexpr int DMA_PER_WAVE = (BLOCKS + NT / 64 - 1) / (NT / 64);
+  static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole 1 KiB blocks");
+  static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS budget");
+};
+
+__device__ __forceinline__ int swz32(int row, int half) { return half ^ ((row >> 3) & 1); }
+
+template <class C, bool KTAIL>
+__global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
+    const uint16_t* __restrict__ xa, int64_t plane_stride, int64_t kp,
+    const int8_t* __restrict__ w, const float* __restrict__ scale,
+    const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n,
+    Epilogue ep, float* __restrict__ y, float* __restrict__ z) {
+  constexpr int BM = C::BM, BN = C::BN, WN = C::WN, PLANES = C::PLANES, STAGES = C::STAGES;
+  constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, BK = C::BK;
+  constexpr int DPW = C::DMA_PER_WAVE;
+  extern __shared__ __align__(16) uint16_t lds_raw[];
+  char* lds = reinterpret_cast<char*>(lds_raw);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int tm, tn;
+  xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
+  const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
+
+  // DMA sources.  Block b (of A_BLOCKS + B_BLOCKS per stage) is handled by
+  // wave b / DPW.  A block: 16 rows x 64 B of one plane; B block: 32 rows x 32 B.
+  const char* src[DPW];
+  int src_koff[DPW];   // byte offset of this lane's chunk inside a stage's K range
+  bool is_b[DPW];
+#pragma unroll
+  for (int j = 0; j < DPW; ++j) {
+    const int blk = min(wave * DPW + j, C::BLOCKS - 1);
+    if (blk < C::A_BLOCKS) {
+      const int r_all = blk * 16 + (lane >> 2);          // row within the PLANES x BM rows
+      const int p = r_all / BM, r = r_all % BM;
+      const int chunk = swz64(r, lane & 3);                 // logical 16-byte chunk
+      int64_t g = m0 + r;
+      g = g < m ? g : m - 1;
+      src[j] = reinterpret_cast<const char*>(xa + p * plane_stride + g * kp);
+      src_koff[j] = chunk * 16;                              // bytes (8 bf16 per chunk)
+      is_b[j] = false;
+    } else {
+      const int r = (blk - C::A_BLOCKS) * 32 + (lane >> 1);
+      const int half = swz32(r, lane & 1);
+      int64_t g = n0 + r;
+      g = g < n ? g : n - 1;
+      src[j] = reinterpret_cast<const char*>(w + g * k);
+      src_koff[j] = half * 16;
+      is_b[j] = true;
+    }
+  }
+  const int ktiles = int(kp / BK);
+  const void* zero = g_zero16;
+  auto issue = [&](int t) {
+    char* dst = lds + (t % STAGES) * C::STAGE_BYTES;
+#pragma unroll
+    for (int j = 0; j < DPW; ++j) {
+      const int blk = min(wave * DPW + j, C::BLOCKS - 1);
+      // A planes hold 2 bytes per K column, B codes 1 byte
+      const void* sp;
+      if (is_b[j]) {
+        const int64_t kb = int64_t(t) * BK + src_koff[j];
+        sp = (KTAIL && kb >= k) ? zero : static_cast<const void*>(src[j] + kb);
+      } else {
+        sp = src[j] + int64_t(t) * BK * 2 + src_koff[j];
+      }
+      dma16(sp, dst + blk * 1024);
+    }
+  };
+  auto wait_stage = [&](int t, int issued) {
+    const int later = (issued < ktiles - 1 ? issued : ktiles - 1) - t;
+    if (later >= 2)
+      wait_vmcnt<2 * DPW>();
+    else if (later == 1)
+      wait_vmcnt<DPW>();
+    else
+      wait_vmcnt<0>();
+  };
+
+  floatx16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int lrow = lane & 31, g = lane >> 5;
+  int a_off[PLANES][FM][2], b_off[FN];
+#pragma unroll
+  for (int p = 0; p < PLANES; ++p)
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int r = wm * TM + i * 32 + lrow;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        a_off[p][i][ks] = (p * BM + r) * 64 + 16 * swz64(r, 2 * g + ks);
+    }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int r = wn * TN + j * 32 + lrow;
+    b_off[j] = C::A_BYTES + r * 32 + 16 * swz32(r, g);
+  }
+  bf16x8 fa[PLANES][FM][2], fb[FN][2];
+  int4 braw[FN];
+  auto read_frags = [&](int t) {
+    const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) braw[j] = *reinterpret_cast<const int4*>(st + b_off[j]);
+#pragma unroll
+    for (int p = 0; p < PLANES; ++p)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          fa[p][i][ks] = *reinterpret_cast<const bf16x8*>(st + a_off[p][i][ks]);
+  };
+  auto expand_b = [&]() {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) codes16_to_bf16(braw[j], fb[j][0], fb[j][1]);
+  };
+  auto mfmas = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int p = 0; p < PLANES; ++p)
+            acc[i][j] = mfma_32x32x16_bf16(fa[p][i][ks], fb[j][ks], acc[i][j]);
+  };
+
+#pragma unroll
+  for (int s0 = 0; s0 < STAGES - 1; ++s0)
+    if (s0 < ktiles) issue(s0);
+  wait_stage(0, STAGES - 2);
+  wait_lgkmcnt0();
+  block_barrier();
+  read_frags(0);
+
+  // per stage: fragments of t are in registers; wait for stage t + 1, let the
+  // ring advance, read t + 1 while the MFMAs of t run.
+  for (int t = 0; t < ktiles; ++t) {
+    wait_lgkmcnt0();
+    expand_b();
+    bf16x8 ca[PLANES][FM][2], cb[FN][2];
+#pragma unroll
+    for (int p = 0; p < PLANES; ++p)
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        ca[p][i][0] = fa[p][i][0];
+        ca[p][i][1] = fa[p][i][1];
+      }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      cb[j][0] = fb[j][0];
+      cb[j][1] = fb[j][1];
+    }
+    if (t + 1 < ktiles) {
+      wait_stage(t + 1, t + STAGES - 2);
+      block_barrier();
+      if (t + STAGES - 1 < ktiles) issue(t + STAGES - 1);
+      sched_fence();
+      read_frags(t + 1);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int p = 0; p < PLANES; ++p)
+            acc[i][j] = mfma_32x32x16_bf16(ca[p][i][ks], cb[j][ks], acc[i][j]);
+    sched_fence();
+  }
+
+  const int lhalf = lane >> 5;
+  with_activation(ep, [&](auto act) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int64_t col = n0 + wn * TN + j * 32 + lrow;
+      if (col >= n) continue;
+      const float s = scale[col];
+      const float b = bias ? bias[col] : 0.f;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * lhalf + (e % 4);
+          if (row < m) {
+            float v = acc[i][j][e] * s;
+            if (bias) v = v + b;
+            if (z) z[row * n + col] = v;
+            y[row * n + col] = act(v);
+          }
+        }
+    }
+  });
+}
+
+template <class C>
+void launch_w8_ring(const uint16_t* xa, int64_t plane_stride, int64_t kp, const int8_t* w,
+                    const float* scale, const float* bias, int64_t m, int64_t n, int64_t k,
+                    const Epilogue& ep, float* y, float* z) {
+  const int64_t tiles_m = ceil_div(m, C::BM), tiles_n = ceil_div(n, C::BN);
+  ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
+  const size_t lds_bytes = size_t(C::STAGES) * C::STAGE_BYTES;
+  static bool attr_set = false;
+  if (!attr_set) {
+    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8_ring_kernel<C, false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
+    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8_ring_kernel<C, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
+    attr_set = true;
+  }
+  auto kernel = (k % C::BK == 0) ? w8_ring_kernel<C, false> : w8_ring_kernel<C, true>;
+  kernel<<<unsigned(tiles_m * tiles_n), C::NT, lds_bytes, stream()>>>(
+      xa, plane_stride, kp, w, scale, bias, m, n, k, int(tiles_m), int(tiles_n), ep, y, z);
+  check_launch("w8_ring_kernel");
+}
+
 template <int BM, int BN, int WM, int WN, int PLANES, int KMODE>
 void launch_gemm(const uint16_t* xa, int64_t plane_stride, int64_t kp, const int8_t* w,
                  int64_t ldw, const float* scale, const float* bias, int64_t m, int64_t n,
@@ -353,7 +613,7 @@ void launch_gemm(const uint16_t* xa, int64_t plane_stride, int64_t kp, const int
     attr_set = true;
   }
   kernel<<<unsigned(tiles_m * tiles_n), WM * WN * 64, lds_bytes, stream()>>>(
-      xa, plane_stride, kp, w, ldw, scale, bias, m, n, k, int(tiles_n), ep, y, z);
+      xa, plane_stride, kp, w, ldw, scale, bias, m, n, k, int(tiles_m), int(tiles_n), ep, y, z);
   check_launch("w8_gemm_kernel");
 }
 
@@ -362,6 +622,50 @@ void gemm_dispatch(const uint16_t* xa, int64_t plane_stride, int64_t kp, const i
                    int64_t ldw, const float* scale, const float* bias, int64_t m, int64_t n,
                    int64_t k, const Epilogue& ep, float* y, float* z) {
   const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256);
+  static const int ring = [] {
+    const char* v = getenv("ENQ_W8_RING");
+    return v ? atoi(v) : 1;
+  }();
+  if (ring && KMODE != 2) {
+    static const int cfg = [] {
+      const char* v = getenv("ENQ_W8_CFG");
+      return v ? atoi(v) : -1;
+    }();
+    // 256 x 256 tiles when they fill the device; otherwise the smallest
+    // tile, whose extra workgroups hide latency better on these shapes
+    const int c = cfg >= 0 ? cfg : (big_tiles >= device_cu_count() ? 9 : 4);
+    switch (c) {
+      case 9:
+        launch_w8_ring<RingCfg<256, 256, 4, 2, PLANES, PLANES == 2 ? 3 : 4>>(
+            xa, plane_stride, kp, w, scale, bias, m, n, k, ep, y, z);
+        break;
+      case 1:
+        launch_w8_ring<RingCfg<128, 128, 4, 2, PLANES, 4>>(xa, plane_stride, kp, w, scale, bias,
+                                                            m, n, k, ep, y, z);
+        break;
+      case 2:
+        launch_w8_ring<RingCfg<64, 128, 2, 2, PLANES, 4>>(xa, plane_stride, kp, w, scale, bias,
+                                                           m, n, k, ep, y, z);
+        break;
+      case 3:
+        launch_w8_ring<RingCfg<128, 64, 2, 2, PLANES, 4>>(xa, plane_stride, kp, w, scale, bias,
+                                                           m, n, k, ep, y, z);
+        break;
+      case 4:
+        launch_w8_ring<RingCfg<64, 64, 2, 2, PLANES, 4>>(xa, plane_stride, kp, w, scale, bias,
+                                                          m, n, k, ep, y, z);
+        break;
+      case 5:
+        launch_w8_ring<RingCfg<128, 256, 2, 4, PLANES, 4>>(xa, plane_stride, kp, w, scale, bias,
+                                                            m, n, k, ep, y, z);
+        break;
+      default:
+        launch_w8_ring<RingCfg<128, 128, 2, 2, PLANES, 4>>(xa, plane_stride, kp, w, scale, bias,
+                                                            m, n, k, ep, y, z);
+        break;
+    }
+    return;
+  }
   if (big_tiles >= device_cu_count())
     launch_gemm<256, 256, 4, 2, PLANES, KMODE>(xa, plane_stride, kp, w, ldw, scale, bias, m, n, k,
                                                ep, y, z);
@@ -373,6 +677,7 @@ void gemm_dispatch(const uint16_t* xa, int64_t plane_stride, int64_t kp, const i
 // Launch geometry of the GEMV: K splits, K chunks per wave, 16-column blocks
 // per block group.
 struct GemvPlan {
+  int64_t m_blocks;  // grid blocks along M (each MB x 16 rows)
   int mb;      // 16-row activation blocks (1, 2 or 4)
   int chunks;  // template bound on K chunks per wave
   int64_t splits;
@@ -383,18 +688,21 @@ struct GemvPlan {
 
 GemvPlan plan_gemv(int64_t m, int64_t n, int64_t kp) {
   GemvPlan g;
-  g.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
-  g.chunks = m <= 16 ? 2 : 1;
+  g.mb = m <= 16 ? 1 : (m <= 32 ? 2 : (m <= 64 ? 4 : 1));
+  g.chunks = g.mb == 1 ? 2 : 1;
+  g.m_blocks = ceil_div(m, g.mb * 16);
   const int64_t chunks_total = ceil_div(kp, kGemvChunk);
   g.splits = ceil_div(chunks_total, int64_t(kGemvWaves) * g.chunks);
   g.chunks_per_wave = int(ceil_div(chunks_total, g.splits * kGemvWaves));
   const int64_t col_blocks = ceil_div(n, 16);
   // enough column groups to fill the device together with the K splits
-  const int64_t want_groups = std::max<int64_t>(1, (int64_t(device_cu_count()) * 2) / g.splits);
+  const int64_t want_groups =
+      std::max<int64_t>(1, (int64_t(device_cu_count()) * 2) / (g.splits * g.m_blocks));
   int cb = int(std::max<int64_t>(1, col_blocks / want_groups));
   g.cb_per_group = std::min(cb, 8);
   g.groups = ceil_div(col_blocks, g.cb_per_group);
-  ENQ_REQUIRE(g.groups <= 0x7fffffff && g.splits <= 65535, "problem too large");
+  ENQ_REQUIRE(g.groups <= 0x7fffffff && g.splits <= 65535 && g.m_blocks <= 65535,
+              "problem too large");
   return g;
 }
 
@@ -402,9 +710,9 @@ template <int MB, int PLANES, int CHUNKS, int KMODE>
 void launch_gemv(const GemvPlan& g, const uint16_t* xa, int64_t plane_stride, int64_t kp,
                  const int8_t* w, int64_t ldw, const float* scale, const float* bias, int64_t m,
                  int64_t n, int64_t k, const Epilogue& ep, float* y, float* z, float* part) {
-  const int64_t mp = MB * 16;
+  const int64_t mp = g.m_blocks * MB * 16;
   gemv_w8_kernel<MB, PLANES, CHUNKS, KMODE>
-      <<<dim3(unsigned(g.groups), unsigned(g.splits)), 512, 0, stream()>>>(
+      <<<dim3(unsigned(g.groups), unsigned(g.splits), unsigned(g.m_blocks)), 512, 0, stream()>>>(
           xa, plane_stride, kp, w, ldw, n, k, g.chunks_per_wave, g.cb_per_group, part);
   check_launch("gemv_w8_kernel");
   const int64_t total = m * n;
@@ -433,17 +741,20 @@ void gemv_dispatch(const GemvPlan& g, const uint16_t* xa, int64_t plane_stride, 
 void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const float* w_scale,
               int64_t n, const float* bias, const Epilogue& ep, int variant, float* y, float* z) {
   const int planes = variant == ENQ_W8_FP32 ? 2 : 1;
-  const bool gemv = m <= 64;
+  // split-K GEMV for few activation rows, and for tall-skinny outputs (one
+  // 16-row block per grid z index, so at most 65535 * 16 rows)
+  const bool gemv = m <= 64 || (n <= kSkinnyN && m <= int64_t(65535) * 16);
   const int64_t kp = ceil_div(k, gemv ? kGemvChunk : kBK) * (gemv ? kGemvChunk : kBK);
-  const int64_t mp = gemv ? (m <= 16 ? 16 : (m <= 32 ? 32 : 64)) : m;
-  const int64_t plane_stride = mp * kp;
-  const size_t planes_bytes = ((size_t(planes) * plane_stride * sizeof(uint16_t)) + 255) / 256 * 256;
   GemvPlan plan{};
   size_t part_bytes = 0;
+  int64_t mp = m;
   if (gemv) {
     plan = plan_gemv(m, n, kp);
+    mp = plan.m_blocks * plan.mb * 16;
     part_bytes = sizeof(float) * size_t(plan.splits) * size_t(mp) * size_t(n);
   }
+  const int64_t plane_stride = mp * kp;
+  const size_t planes_bytes = ((size_t(planes) * plane_stride * sizeof(uint16_t)) + 255) / 256 * 256;
   // one allocation for everything this call needs, taken before any launch
   char* ws = static_cast<char*>(workspace(planes_bytes + part_bytes));
   auto* xa = reinterpret_cast<uint16_t*>(ws);

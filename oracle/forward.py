@@ -136,6 +136,9 @@ def top_k(probs: Any, k: int) -> Any:
     return np.argsort(-probs, axis=-1)[:, :k]
 
 
+forward_top_k = top_k
+
+
 def moe_forward(x: Any, layer: Dict[str, Any],
                 probs: Optional[Any] = None) -> Any:
     """Mixture-of-Experts forward.  Follows ``nn/moe.py:52-87`` minus the

@@ -4,6 +4,8 @@
   is the float64 product of the activations with the fake-quantized weights
   (the reference's Dense, ``nn/forward.py:318-319``).
 * W8 bf16 variant: the same bound at 2e-2.
+* A single output column (n = 1) is bounded against sum_k |x_k w_k| instead of
+  |z|, since the row bound there fails for any float32 dot product.
 * W8A8: int32 accumulators, activation codes and scales bit-identical to the
   oracle; the linear fp32 output too (same operation order, no FMA).
 """
@@ -40,7 +42,9 @@ def row_rel_err(got, ref):
 
 SHAPES = [(1, 512, 512), (3, 100, 10), (16, 8192, 1024), (16, 784, 1024), (17, 1024, 300),
           (33, 512, 100), (64, 512, 512), (65, 784, 1024), (100, 100, 37), (256, 1024, 1024),
-          (300, 784, 1024), (512, 4096, 1024), (1000, 1024, 10), (4, 16, 1), (129, 48, 260)]
+          (300, 784, 1024), (512, 4096, 1024), (1000, 1024, 10), (4, 16, 1), (129, 48, 260),
+          # tall-skinny outputs (GEMV over 16-row blocks): ragged K, n = 1, n = 32
+          (4096, 1024, 10), (2000, 100, 1), (70, 30, 32), (77, 130, 17)]
 
 
 @pytest.mark.parametrize("m,k,n", SHAPES)
@@ -54,7 +58,16 @@ def test_dense_w8_pre_activation(gpu, m, k, n, variant, tol):
     y = D.dense_w8(d_x, wq, d_b, "linear", variant=variant, pre_activation=z)
     zh, yh = z.numpy(), y.numpy()
     assert np.array_equal(zh, yh)
-    err = row_rel_err(zh.astype(np.float64), z_ref)
+    if n == 1:
+        # One output per row: the row bound becomes a relative bound on a
+        # single dot product, which no float32 evaluation meets under
+        # cancellation (the reference's own float32 x @ W misses it on 2 of
+        # these 2000 rows).  Bound the error by the magnitude of the terms
+        # instead: |z - z_ref| <= tol * sum_k |x_k * w_k|.
+        terms = np.abs(x.astype(np.float64)) @ np.abs(fq.astype(np.float64)).T
+        err = (np.abs(zh.astype(np.float64) - z_ref) / np.maximum(terms, 1e-30)).max(axis=-1)
+    else:
+        err = row_rel_err(zh.astype(np.float64), z_ref)
     assert np.all(err <= tol), f"max row error {err.max():.3e} > {tol}"
 
 
