@@ -33,6 +33,7 @@ import numpy as np
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA
 INT8_PEAK_TOPS = 5000.0        # dense int8 MFMA
+FP32_PEAK_TFLOPS = 157.3       # fp32 MFMA
 
 
 def measured_traffic(name, shape):
@@ -305,7 +306,110 @@ def components(timer, rng, only):
         tops = 2.0 * 8192 * nk / ms / 1e9
         out["gemm_w8a8_8192cubed"] = {"ms": ms, "TOP/s": tops,
                                       "frac_int8_peak": tops / INT8_PEAK_TOPS}
+        del xsq, ysq
+    del wq, d_codes, d_scale, x4, y4
+    if on("transformer_block"):
+        out.update(transformer_block(timer, rng))
+    if on("moe"):
+        out.update(moe_layer(timer, rng))
     return out
+
+
+def transformer_block(timer, rng):
+    """one pre-norm transformer block on x (8, 512,
+    1024), 16 heads of 64, FFN 4096 with GELU, weights N(0, 0.02) quantized
+    per output channel, zero biases, LayerNorm gamma 1 beta 0.  The metric
+    counts the weight GEMMs only (QKV, O, FFN1, FFN2: 103.08 GFLOP); the fp32
+    attention core (8.59 GFLOP) is timed on its own as well."""
+    from enilnets_amd import _lib, quantize_weights
+    from enilnets_amd.device import DeviceArray
+    from enilnets_amd.nn import Model, int8_weights
+    from enilnets_amd.nn import transformer as T
+    from enilnets_amd.nn.dense import dense_w8
+    B, S, E, F, H = 8, 512, 1024, 4096, 16
+    m = Model()
+    m.add_residual_start()
+    m.add_layernorm(E)
+    ws = [rng.normal(0.0, 0.02, (E, E)).astype(np.float32) for _ in range(4)]
+    m.add_multihead_attention(*ws, num_heads=H)
+    m.add_residual_end()
+    m.add_residual_start()
+    m.add_layernorm(E)
+    m.add_dense(rng.normal(0.0, 0.02, (F, E)).astype(np.float32), np.zeros(F, np.float32), "gelu")
+    m.add_dense(rng.normal(0.0, 0.02, (E, F)).astype(np.float32), np.zeros(E, np.float32),
+                "linear")
+    m.add_residual_end()
+    quantize_weights(m, bits=8, per_channel=True)
+    L = m.layers
+    x = DeviceArray.from_numpy(rng.standard_normal((B, S, E)).astype(np.float32))
+    ln1, ln2 = T.layernorm_params(L[1]), T.layernorm_params(L[5])
+    plan = T.MhaPlan(L[2], B, S)
+    w1, w2 = int8_weights(L[6], "weights"), int8_weights(L[7], "weights")
+    b1, b2 = DeviceArray.from_numpy(L[6]["bias"]), DeviceArray.from_numpy(L[7]["bias"])
+    t1, a1, r1, t2, f2, y = (DeviceArray((B, S, E), np.float32) for _ in range(6))
+    h = DeviceArray((B, S, F), np.float32)
+
+    def block(_=0):
+        T.layernorm(x, L[1], out=t1, params=ln1)
+        T.mha_forward(t1, L[2], plan=plan, out=a1)
+        T.residual_add(a1, x, out=r1)
+        T.layernorm(r1, L[5], out=t2, params=ln2)
+        dense_w8(t2, w1, b1, "gelu", out=h)
+        dense_w8(h, w2, b2, "linear", out=f2)
+        T.residual_add(f2, r1, out=y)
+
+    block()
+    ms = timer.time(block, 10)
+    flops = 2.0 * B * S * (3 * E * E + E * E + E * F + F * E)
+    res = {"transformer_block_b8_s512_e1024": {
+        "ms": ms, "TFLOP/s": flops / ms / 1e9, "frac_bf16_peak": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
+        "weight_gflop": flops / 1e9, "variant": "fp32"}}
+    n_all = plan.wqkv.shape[0]
+
+    def core(_=0):
+        _lib.call("enq_attention", plan.qkv.ptr, n_all, T._at(plan.qkv, 4 * E), n_all,
+                  T._at(plan.qkv, 8 * E), n_all, B, S, H, H, E // H, 0, -1, plan.ctx.ptr, E)
+
+    core()
+    ms = timer.time(core, 20)
+    aflops = 4.0 * B * H * S * S * (E // H)
+    res["attention_core_b8_s512_h16_d64"] = {
+        "ms": ms, "TFLOP/s": aflops / ms / 1e9, "frac_fp32_peak": aflops / ms / 1e9 / FP32_PEAK_TFLOPS}
+    return res
+
+
+def moe_layer(timer, rng):
+    """8192 tokens x 1024, router logits (8192, 8)
+    N(0, 1) given, top-2 with raw-probability gates, W1 (8, 4096, 1024) and
+    W2 (8, 1024, 4096) N(0, 0.02) quantized per output channel within each
+    expert slice, zero biases, GELU; 274.88 GFLOP per call."""
+    from enilnets_amd.device import DeviceArray
+    from enilnets_amd.nn import Int8Weights
+    from enilnets_amd.nn.dense import quantize_weight_rows
+    from enilnets_amd.nn.moe import moe_forward
+    T_, D, Hd, E_, K_ = 8192, 1024, 4096, 8, 2
+    layer = {"type": "moe", "embed_dim": D, "num_experts": E_, "hidden_dim": Hd, "top_k": K_,
+             "activation": "gelu"}
+    weights = []
+    for shape in ((E_, Hd, D), (E_, D, Hd)):
+        w = rng.normal(0.0, 0.02, shape).astype(np.float32)
+        rows = quantize_weight_rows(w.reshape(-1, shape[2]))  # per row of each expert slice
+        weights.append(Int8Weights(rows.codes, rows.scale, shape, 8, True, None, None))
+        del w
+    x = DeviceArray.from_numpy(rng.standard_normal((T_, D)).astype(np.float32))
+    logits = DeviceArray.from_numpy(rng.standard_normal((T_, E_)).astype(np.float32))
+    y = DeviceArray((T_, D), np.float32)
+    _, info = moe_forward(x, layer, router_logits=logits, want_routing=True, out=y,
+                          biases=(None, None, None), aux_loss=False,
+                          weights=(weights[0], weights[1], None))
+    counts = np.bincount(info["top_idx"].numpy().reshape(-1), minlength=E_)
+    f = lambda i: moe_forward(x, layer, router_logits=logits, out=y, biases=(None, None, None),
+                              aux_loss=False, weights=(weights[0], weights[1], None))
+    ms = timer.time(f, 5)
+    flops = 2.0 * T_ * K_ * D * Hd * 2
+    return {"moe_t8192_e8_top2_d1024_h4096": {
+        "ms": ms, "TFLOP/s": flops / ms / 1e9, "frac_bf16_peak": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
+        "gflop": flops / 1e9, "rows_per_expert": counts.tolist(), "variant": "fp32"}}
 
 
 def main():

@@ -87,6 +87,13 @@ SIGNATURES = {
                               c_float, _P, _P]),
     "enq_dense_w8a8": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, _P, c_int, c_float,
                                c_float, _P, _P]),
+    "enq_layernorm": (c_int, [_P, c_int64, c_int64, _P, _P, c_float, _P]),
+    "enq_add": (c_int, [_P, _P, c_int64, _P]),
+    "enq_attention": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, c_int64, c_int64, c_int,
+                              c_int, c_int, c_int, c_int64, _P, c_int64]),
+    "enq_moe_w8": (c_int, [_P, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                           c_int64, c_int64, c_int, c_int, c_float, c_float, c_int, _P, _P, _P,
+                           _P]),
 }
 
 _lock = threading.RLock()

@@ -1,0 +1,367 @@
+// The non-GEMM pieces of a transformer block on the quantized path:
+// LayerNorm over the last axis (Enilnets/nn/forward.py:207-254), the residual
+// add (forward.py:762-766) and the softmax attention core between the
+// projections of the multi-head attention layer (forward.py:423-436,525-549).
+//
+// attention_kernel: one workgroup per (64 queries, head, batch), four waves
+// of 16 queries.  Each 64-key block of K and V is staged in LDS; a wave forms
+// S^T = K . Q^T (keys x queries) with fp32 MFMA 16x16x4, so every lane owns
+// one query's column and the softmax statistics are per lane; masks,
+// running max and the rescale follow; then O^T += V^T . P^T reuses the score
+// registers directly as the B operand.  Everything is fp32: products are
+// exact fp32 products, sums fp32.
+#include <cmath>
+
+#include "common.hpp"
+#include "mfma.hpp"
+
+namespace enq {
+namespace {
+
+// ---------------------------------------------------------------------------
+// LayerNorm: y = gamma * (x - mean) / sqrt(var + eps) + beta per row, with the
+// mean and the (biased) variance of the row, two passes over values held in
+// registers.  One 256-thread workgroup per row; PER values per thread.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();  // red may still be read from the previous reduction
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+template <int PER>
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, int64_t cols,
+                                                        const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta, float eps,
+                                                        float* __restrict__ y) {
+  __shared__ float red[4];
+  const float* xr = x + int64_t(blockIdx.x) * cols;
+  float* yr = y + int64_t(blockIdx.x) * cols;
+  float v[PER];
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t c = int64_t(i) * 256 + threadIdx.x;
+    v[i] = c < cols ? xr[c] : 0.0f;
+    s += v[i];
+  }
+  const float mean = block_sum256(s, red) / float(cols);
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t c = int64_t(i) * 256 + threadIdx.x;
+    const float dlt = c < cols ? v[i] - mean : 0.0f;
+    q += dlt * dlt;
+  }
+  const float var = block_sum256(q, red) / float(cols);
+  const float den = sqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t c = int64_t(i) * 256 + threadIdx.x;
+    if (c < cols) yr[c] = gamma[c] * ((v[i] - mean) / den) + beta[c];
+  }
+}
+
+// Rows longer than 256 * 16: the same arithmetic, re-reading the row.
+__global__ __launch_bounds__(256) void layernorm_long_kernel(const float* __restrict__ x,
+                                                             int64_t cols,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta,
+                                                             float eps, float* __restrict__ y) {
+  __shared__ float red[4];
+  const float* xr = x + int64_t(blockIdx.x) * cols;
+  float* yr = y + int64_t(blockIdx.x) * cols;
+  float s = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) s += xr[c];
+  const float mean = block_sum256(s, red) / float(cols);
+  float q = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float dlt = xr[c] - mean;
+    q += dlt * dlt;
+  }
+  const float den = sqrtf(block_sum256(q, red) / float(cols) + eps);
+  for (int64_t c = threadIdx.x; c < cols; c += 256)
+    yr[c] = gamma[c] * ((xr[c] - mean) / den) + beta[c];
+}
+
+__global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a,
+                                                  const float* __restrict__ b, int64_t n,
+                                                  float* __restrict__ y) {
+  const int64_t i4 = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i4 + 4 <= n) {
+    const float4 p = *reinterpret_cast<const float4*>(a + i4);
+    const float4 q = *reinterpret_cast<const float4*>(b + i4);
+    *reinterpret_cast<float4*>(y + i4) = make_float4(p.x + q.x, p.y + q.y, p.z + q.z, p.w + q.w);
+  } else {
+    for (int64_t i = i4; i < n; ++i) y[i] = a[i] + b[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Attention core
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ floatx4 mfma_16x16x4_f32(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+struct AttnShape {
+  int64_t batch, seq;
+  int heads, kv_heads;
+  int64_t ldq, ldk, ldv, ldo;  // row strides (elements)
+  float scale;                 // 1 / sqrt(head_dim)
+  int causal;
+  int64_t window;              // < 0: unbounded
+};
+
+constexpr int kAttnQ = 64;   // queries per workgroup (4 waves x 16)
+constexpr int kAttnKB = 64;  // keys per LDS block
+
+template <int DH>
+__global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ q,
+                                                        const float* __restrict__ k,
+                                                        const float* __restrict__ v,
+                                                        AttnShape sh, float* __restrict__ out) {
+  constexpr int PITCH = DH + 4;     // LDS row pitch (floats): conflict-free reads
+  constexpr int DG = DH / 4;        // dims per lane group in the S^T steps
+  constexpr int DT = DH / 16;       // 16-dim output tiles
+  __shared__ __align__(16) float kt[kAttnKB * PITCH];
+  __shared__ __align__(16) float vt[kAttnKB * PITCH];
+  __shared__ __align__(16) float ot[4][16 * PITCH];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int64_t b = blockIdx.z;
+  const int h = blockIdx.y;
+  const int kvh = h / (sh.heads / sh.kv_heads);
+  const int64_t qblk0 = int64_t(blockIdx.x) * kAttnQ;
+  const int64_t qi = qblk0 + wave * 16 + col;  // this lane's query
+  const int64_t S = sh.seq;
+  const float* qb = q + (b * S) * sh.ldq + int64_t(h) * DH;
+  const float* kb = k + (b * S) * sh.ldk + int64_t(kvh) * DH;
+  const float* vb = v + (b * S) * sh.ldv + int64_t(kvh) * DH;
+
+  // Q^T operand: step st of lane group g uses dim g * DG + st.
+  float qreg[DG];
+  {
+    const float* src = qb + (qi < S ? qi : 0) * sh.ldq + grp * DG;
+#pragma unroll
+    for (int c = 0; c < DG / 4; ++c) {
+      const float4 t = qi < S ? *reinterpret_cast<const float4*>(src + 4 * c)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+      qreg[4 * c] = t.x;
+      qreg[4 * c + 1] = t.y;
+      qreg[4 * c + 2] = t.z;
+      qreg[4 * c + 3] = t.w;
+    }
+  }
+
+  floatx4 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;  // running max of this lane's query
+  float l_part = 0.0f;      // this lane's share of the running sum
+
+  // key blocks that can hold an allowed key for any query of the workgroup
+  const int64_t q_last = (qblk0 + kAttnQ - 1 < S - 1) ? qblk0 + kAttnQ - 1 : S - 1;
+  int64_t key_end = S;
+  if (sh.causal) key_end = q_last + 1;
+  if (sh.window >= 0 && q_last + sh.window + 1 < key_end) key_end = q_last + sh.window + 1;
+  int64_t key_begin = 0;
+  if (sh.window >= 0 && qblk0 - sh.window > 0) key_begin = qblk0 - sh.window;
+  const int64_t kb_begin = key_begin / kAttnKB;
+  const int64_t kb_end = (key_end + kAttnKB - 1) / kAttnKB;
+
+  for (int64_t blk = kb_begin; blk < kb_end; ++blk) {
+    const int64_t key0 = blk * kAttnKB;
+    __syncthreads();  // previous block's K/V reads are done
+    // stage 64 keys x DH of K and V (float4 per thread per step); rows past
+    // the sequence are zero so masked products stay finite
+    for (int idx = threadIdx.x; idx < kAttnKB * DH / 4; idx += 256) {
+      const int r = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+      const int64_t key = key0 + r;
+      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+      if (key < S) {
+        kv = *reinterpret_cast<const float4*>(kb + key * sh.ldk + c4);
+        vv = *reinterpret_cast<const float4*>(vb + key * sh.ldv + c4);
+      }
+      *reinterpret_cast<float4*>(&kt[r * PITCH + c4]) = kv;
+      *reinterpret_cast<float4*>(&vt[r * PITCH + c4]) = vv;
+    }
+    __syncthreads();
+
+    // S^T: 4 subtiles of 16 keys; lane holds keys 16 ks + 4 grp + i of query qi
+    floatx4 s[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      s[ks] = floatx4{0.f, 0.f, 0.f, 0.f};
+      const float* krow = &kt[(ks * 16 + col) * PITCH + grp * DG];
+#pragma unroll
+      for (int c = 0; c < DG / 4; ++c) {
+        const float4 a4 = *reinterpret_cast<const float4*>(krow + 4 * c);
+        s[ks] = mfma_16x16x4_f32(a4.x, qreg[4 * c], s[ks]);
+        s[ks] = mfma_16x16x4_f32(a4.y, qreg[4 * c + 1], s[ks]);
+        s[ks] = mfma_16x16x4_f32(a4.z, qreg[4 * c + 2], s[ks]);
+        s[ks] = mfma_16x16x4_f32(a4.w, qreg[4 * c + 3], s[ks]);
+      }
+    }
+    // scale, mask, block max
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t key = key0 + ks * 16 + 4 * grp + i;
+        bool blocked = key >= S;
+        if (sh.causal) blocked = blocked || key > qi;
+        if (sh.window >= 0) {
+          const int64_t dlt = qi - key;
+          blocked = blocked || (dlt > sh.window || -dlt > sh.window);
+        }
+        const float val = blocked ? -INFINITY : s[ks][i] * sh.scale;
+        s[ks][i] = val;
+        mx = fmaxf(mx, val);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = expf(m_run - m_use);
+    m_run = m_new;
+    float psum = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = expf(s[ks][i] - m_use);
+        s[ks][i] = p;
+        psum += p;
+      }
+    l_part = l_part * alpha + psum;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] *= alpha;
+
+    // O^T += V^T . P^T: step (ks, i) of lane group g is key 16 ks + 4 g + i
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float* vrow = &vt[(ks * 16 + 4 * grp + i) * PITCH + col];
+#pragma unroll
+        for (int t = 0; t < DT; ++t) o[t] = mfma_16x16x4_f32(vrow[16 * t], s[ks][i], o[t]);
+      }
+  }
+
+  // total sum over the four lanes of this query; normalise; write through
+  // LDS so each query row leaves as contiguous float4 stores
+  float l_tot = l_part + __shfl_xor(l_part, 16, 64);
+  l_tot = l_tot + __shfl_xor(l_tot, 32, 64);
+  float* my = ot[wave];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) my[col * PITCH + t * 16 + 4 * grp + r] = o[t][r] / l_tot;
+  __syncthreads();
+  for (int idx = lane; idx < 16 * (DH / 4); idx += 64) {
+    const int r = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+    const int64_t qq = qblk0 + wave * 16 + r;
+    if (qq < S)
+      *reinterpret_cast<float4*>(out + (b * S + qq) * sh.ldo + int64_t(h) * DH + c4) =
+          *reinterpret_cast<const float4*>(&my[r * PITCH + c4]);
+  }
+}
+
+void attention(const float* q, const float* k, const float* v, const AttnShape& sh, int head_dim,
+               float* out) {
+  const dim3 grid(unsigned(ceil_div(sh.seq, kAttnQ)), unsigned(sh.heads), unsigned(sh.batch));
+  switch (head_dim) {
+    case 16:
+      attention_kernel<16><<<grid, 256, 0, stream()>>>(q, k, v, sh, out);
+      break;
+    case 32:
+      attention_kernel<32><<<grid, 256, 0, stream()>>>(q, k, v, sh, out);
+      break;
+    case 64:
+      attention_kernel<64><<<grid, 256, 0, stream()>>>(q, k, v, sh, out);
+      break;
+    case 128:
+      attention_kernel<128><<<grid, 256, 0, stream()>>>(q, k, v, sh, out);
+      break;
+    default:
+      fail(ENQ_ERR_UNSUPPORTED, "attention head_dim %d is not one of 16, 32, 64, 128", head_dim);
+  }
+  check_launch("attention_kernel");
+}
+
+}  // namespace
+}  // namespace enq
+
+using namespace enq;
+
+extern "C" int enq_layernorm(const float* x, int64_t rows, int64_t cols, const float* gamma,
+                             const float* beta, float eps, float* y) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(rows >= 1 && cols >= 1, "rows and cols must be positive");
+    ENQ_REQUIRE(x && gamma && beta && y, "NULL pointer argument");
+    ENQ_REQUIRE(rows <= 0x7fffffff, "too many rows");
+    const unsigned grid = unsigned(rows);
+    hipStream_t s = stream();
+    if (cols <= 256 * 1)
+      layernorm_kernel<1><<<grid, 256, 0, s>>>(x, cols, gamma, beta, eps, y);
+    else if (cols <= 256 * 2)
+      layernorm_kernel<2><<<grid, 256, 0, s>>>(x, cols, gamma, beta, eps, y);
+    else if (cols <= 256 * 4)
+      layernorm_kernel<4><<<grid, 256, 0, s>>>(x, cols, gamma, beta, eps, y);
+    else if (cols <= 256 * 8)
+      layernorm_kernel<8><<<grid, 256, 0, s>>>(x, cols, gamma, beta, eps, y);
+    else if (cols <= 256 * 16)
+      layernorm_kernel<16><<<grid, 256, 0, s>>>(x, cols, gamma, beta, eps, y);
+    else
+      layernorm_long_kernel<<<grid, 256, 0, s>>>(x, cols, gamma, beta, eps, y);
+    check_launch("layernorm_kernel");
+  });
+}
+
+extern "C" int enq_add(const float* a, const float* b, int64_t n, float* y) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return;
+    ENQ_REQUIRE(a && b && y, "NULL pointer argument");
+    ENQ_REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(y, 16),
+                "enq_add needs 16-byte aligned buffers");
+    const int64_t blocks = ceil_div(ceil_div(n, 4), 256);
+    ENQ_REQUIRE(blocks <= 0x7fffffff, "problem too large");
+    add_kernel<<<unsigned(blocks), 256, 0, stream()>>>(a, b, n, y);
+    check_launch("add_kernel");
+  });
+}
+
+extern "C" int enq_attention(const float* q, int64_t ldq, const float* k, int64_t ldk,
+                             const float* v, int64_t ldv, int64_t batch, int64_t seq, int heads,
+                             int kv_heads, int head_dim, int causal, int64_t window, float* out,
+                             int64_t ldo) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(batch >= 1 && seq >= 1 && heads >= 1 && kv_heads >= 1,
+                "batch, seq, heads and kv_heads must be positive");
+    ENQ_REQUIRE(heads % kv_heads == 0, "heads (%d) must be a multiple of kv_heads (%d)", heads,
+                kv_heads);
+    ENQ_REQUIRE(q && k && v && out, "NULL pointer argument");
+    ENQ_REQUIRE(batch <= 65535 && heads <= 65535 && ceil_div(seq, kAttnQ) <= 0x7fffffff,
+                "problem too large");
+    ENQ_REQUIRE(ldq >= int64_t(heads) * head_dim && ldo >= int64_t(heads) * head_dim &&
+                    ldk >= int64_t(kv_heads) * head_dim && ldv >= int64_t(kv_heads) * head_dim,
+                "row strides smaller than the heads they hold");
+    ENQ_REQUIRE(ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && ldo % 4 == 0 &&
+                    aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 16),
+                "attention needs 16-byte aligned rows");
+    AttnShape sh{batch, seq, heads, kv_heads, ldq, ldk, ldv, ldo,
+                 float(1.0 / std::sqrt(double(head_dim))), causal ? 1 : 0, window};
+    attention(q, k, v, sh, head_dim, out);
+  });
+}

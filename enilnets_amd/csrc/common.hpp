@@ -61,7 +61,12 @@ int device_cu_count();
 // Growable per-device scratch memory for partial results.  A call may use
 // `bytes` of it until it returns; calls on the library stream are ordered,
 // so reuse across calls is safe.  Growing synchronizes the stream first.
-void* workspace(size_t bytes);
+// Slot kKernelSlot belongs to the single-operation entry points (dense, W8A8,
+// quantize); kLayerSlot to layer-level entry points (attention, MoE) that
+// call those operations while their own buffers stay live.
+constexpr int kKernelSlot = 0;
+constexpr int kLayerSlot = 1;
+void* workspace(size_t bytes, int slot = kKernelSlot);
 
 // Checks the launch that was just enqueued.
 void check_launch(const char* what);

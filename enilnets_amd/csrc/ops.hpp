@@ -1,0 +1,35 @@
+// Internal entry points shared between translation units: the W8 Dense
+// pieces that the layer-level operations (attention, mixture of experts)
+// compose.
+#pragma once
+
+#include <cstdint>
+
+#include "epilogue.hpp"
+#include "tiling.hpp"
+
+namespace enq {
+
+// act(x @ (codes * w_scale).T + bias), fp32 x of shape (m, k); z receives the
+// pre-activation when non-null.  Uses the kernel workspace slot.
+void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const float* w_scale,
+              int64_t n, const float* bias, const Epilogue& ep, int variant, float* y, float* z);
+
+// x rows (gathered through `gather` when non-null) -> `planes` bf16 planes of
+// shape (mp, kp), zero padded; plane p starts at xa + p * mp * kp.
+void split_planes(const float* x, const int* gather, int64_t m, int64_t k, uint16_t* xa,
+                  int64_t mp, int64_t kp, int planes);
+
+// K padding of the planes the LDS-tiled GEMM reads.
+int64_t gemm_k_pad(int64_t k);
+
+// Whether the grouped GEMM takes weights of this K and alignment.
+bool grouped_gemm_supported(int64_t k, const int8_t* codes);
+
+// GEMM over pre-split planes with rows in groups (`grp`), group g using
+// codes + g * grp.w_stride and w_scale / bias + g * grp.v_stride.
+void dense_w8_grouped(const uint16_t* xa, int64_t plane_stride, int64_t kp, int planes,
+                      int64_t m, int64_t k, const int8_t* codes, const float* w_scale, int64_t n,
+                      const float* bias, const RowGroups& grp, const Epilogue& ep, float* y);
+
+}  // namespace enq

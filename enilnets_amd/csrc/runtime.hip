@@ -17,8 +17,8 @@ struct DeviceState {
   int cu_count = 0;
   hipStream_t own_stream = nullptr;
   hipStream_t user_stream = nullptr;  // enq_set_stream
-  void* workspace = nullptr;
-  size_t workspace_bytes = 0;
+  void* workspace[2] = {nullptr, nullptr};
+  size_t workspace_bytes[2] = {0, 0};
 };
 
 DeviceState g_state;
@@ -61,22 +61,23 @@ hipStream_t stream() {
 
 int device_cu_count() { return g_state.cu_count; }
 
-void* workspace(size_t bytes) {
+void* workspace(size_t bytes, int slot) {
   std::lock_guard<std::mutex> lock(g_mutex);
-  if (bytes <= g_state.workspace_bytes) return g_state.workspace;
+  if (slot != kKernelSlot && slot != kLayerSlot) fail(ENQ_ERR_RUNTIME, "bad workspace slot");
+  if (bytes <= g_state.workspace_bytes[slot]) return g_state.workspace[slot];
   // Round up so repeated small growth does not reallocate every call.
   size_t want = 1u << 20;
   while (want < bytes) want <<= 1;
-  if (g_state.workspace) {
+  if (g_state.workspace[slot]) {
     // Earlier work on the stream may still read the old buffer.
     ENQ_HIP(hipStreamSynchronize(stream()));
-    ENQ_HIP(hipFree(g_state.workspace));
-    g_state.workspace = nullptr;
-    g_state.workspace_bytes = 0;
+    ENQ_HIP(hipFree(g_state.workspace[slot]));
+    g_state.workspace[slot] = nullptr;
+    g_state.workspace_bytes[slot] = 0;
   }
-  ENQ_HIP(hipMalloc(&g_state.workspace, want));
-  g_state.workspace_bytes = want;
-  return g_state.workspace;
+  ENQ_HIP(hipMalloc(&g_state.workspace[slot], want));
+  g_state.workspace_bytes[slot] = want;
+  return g_state.workspace[slot];
 }
 
 void check_launch(const char* what) {
@@ -114,7 +115,8 @@ int enq_init(int device) {
     if (g_state.ready) {
       ENQ_HIP(hipStreamSynchronize(g_state.own_stream));
       ENQ_HIP(hipStreamDestroy(g_state.own_stream));
-      if (g_state.workspace) ENQ_HIP(hipFree(g_state.workspace));
+      for (void* w : g_state.workspace)
+        if (w) ENQ_HIP(hipFree(w));
       g_state = DeviceState{};
     }
     ENQ_HIP(hipSetDevice(device));

@@ -27,6 +27,34 @@ __device__ __forceinline__ void xcd_tile(int bid, int tiles_m, int tiles_n, int 
   tn = in_group / rows;
 }
 
+// Rows split into consecutive groups (the tokens routed to each expert),
+// each multiplied by its own weight matrix.  Every group is tiled on its own,
+// so a tile never straddles two groups.
+struct RowGroups {
+  const int* offsets = nullptr;  // groups + 1 ascending row offsets (device)
+  int groups = 0;
+  int64_t w_stride = 0;          // weight elements from one group to the next
+  int64_t v_stride = 0;          // scale and bias elements from one group to the next
+};
+
+// Group of virtual tile row `tm` and the rows [m0, m_end) of that tile's
+// group; -1 past the last group's tiles.  Uniform across a workgroup.
+__device__ inline int group_tile(const RowGroups& g, int bm, int tm, int64_t& m0,
+                                 int64_t& m_end) {
+  int base = 0;
+  for (int e = 0; e < g.groups; ++e) {
+    const int r0 = g.offsets[e], r1 = g.offsets[e + 1];
+    const int t = (r1 - r0 + bm - 1) / bm;
+    if (tm < base + t) {
+      m0 = r0 + int64_t(tm - base) * bm;
+      m_end = r1;
+      return e;
+    }
+    base += t;
+  }
+  return -1;
+}
+
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at "no wait").
 template <int N>

@@ -1,7 +1,7 @@
 """Device memory owned by libenilnets_amd.
 
 ``DeviceArray`` is a dense, row-major array in HBM with a NumPy dtype and
-shape.  It is what the device-resident API (``enilnets_amd.nn.layers``) and
+shape.  It is what the device-resident API (``enilnets_amd.nn``) and
 the benchmark keep between calls; the NumPy drop-in functions create and
 release them per call.
 """

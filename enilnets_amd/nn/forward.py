@@ -4,9 +4,10 @@ Mirrors ``Enilnets/nn/forward.py:272-811`` for the layer types of the
 quantized-inference path: the input is cast to float32 (the reference's
 default working dtype, ``:285``), every layer runs on the device, and
 ``model.outputs`` / ``model.pre_activations`` are filled with host arrays as
-the reference fills them (``:295-302,810``).  Dense layers run on their int8
-codes (``enilnets_amd.nn.weights``).  Layer types outside this path raise
-NotImplementedError instead of silently computing on the host.
+the reference fills them (``:295-302,810``).  Dense, attention-projection
+and expert weights run on their int8 codes (``enilnets_amd.nn.weights``).
+Layer types outside this path raise NotImplementedError instead of silently
+computing on the host.
 """
 
 from typing import Any, Dict, List, Optional
@@ -16,6 +17,8 @@ import numpy as np
 from .. import _lib
 from ..device import DeviceArray
 from .dense import dense_w8
+from .moe import moe_forward
+from .transformer import layernorm, mha_forward, residual_add
 from .weights import int8_weights
 
 #: Activations whose NumPy result is float64 for a float32 input, because
@@ -48,12 +51,29 @@ def _fake_quantize_device(x: DeviceArray, spec: Dict[str, Any]) -> DeviceArray:
     return out
 
 
+def _dense(cur: DeviceArray, layer: Dict[str, Any], variant: str):
+    w = int8_weights(layer, "weights")
+    n = w.shape[0]
+    z = DeviceArray(cur.shape[:-1] + (n,), np.float32)
+    y = dense_w8(cur, w, _bias(layer, "bias", n), layer["activation"],
+                 layer.get("activation_params", {}), variant, pre_activation=z)
+    dtype = np.float64 if layer["activation"] in _FLOAT64_ACTIVATIONS else np.float32
+    return y, z, dtype
+
+
 def Forward(model: Any, inputs: Any, training: bool = False, dropout_rate: float = 0.0,
             variant: str = "fp32") -> np.ndarray:
     """Run ``inputs`` through ``model.layers`` on the GPU.  Returns the last
     layer's output and fills ``model.outputs`` and ``model.pre_activations``
     like the reference.  ``variant`` selects the W8 Dense arithmetic
-    ("fp32": fp32-accurate, "bf16": bf16 activations)."""
+    ("fp32": fp32-accurate, "bf16": bf16 activations).
+
+    Layer types: dense/sparse, layernorm, multihead_attention (softmax),
+    residual_save, residual_add and moe.  Every layer computes in float32 on
+    the device; the host copy of each output takes the dtype NumPy gives the
+    reference's expression (float64 after GELU, ``forward.py:32``; after
+    attention, whose scores are divided by the float64 ``np.sqrt(Dh)``,
+    ``:525``; and wherever a float64 operand propagates)."""
     x = np.asarray(inputs, dtype=np.float32)
     if x.ndim == 1:
         x = x.reshape(1, -1)
@@ -62,27 +82,41 @@ def Forward(model: Any, inputs: Any, training: bool = False, dropout_rate: float
     dev: List[DeviceArray] = [DeviceArray.from_numpy(x)]
     for layer in model.layers:
         cur = dev[-1]
+        cur_dtype = outputs[-1].dtype
         kind = layer["type"]
         z_host = None
         if kind in ("dense", "sparse"):
-            w = int8_weights(layer, "weights")
-            n = w.shape[0]
-            z = DeviceArray(cur.shape[:-1] + (n,), np.float32)
-            y = dense_w8(cur, w, _bias(layer, "bias", n), layer["activation"],
-                         layer.get("activation_params", {}), variant, pre_activation=z)
+            y, z, dtype = _dense(cur, layer, variant)
             z_host = z.numpy()
-            host = y.numpy()
-            if layer["activation"] in _FLOAT64_ACTIVATIONS:
-                host = host.astype(np.float64)
+        elif kind == "layernorm":
+            y = layernorm(cur, layer)
+            dtype = np.result_type(cur_dtype, np.asarray(layer["gamma"]).dtype,
+                                   np.asarray(layer["beta"]).dtype)
+        elif kind == "multihead_attention":
+            y = mha_forward(cur, layer, variant, training)
+            dtype = np.float64
         elif kind == "residual_save":
-            y, host = cur, outputs[-1]
+            y, dtype = cur, cur_dtype
+        elif kind == "residual_add":
+            idx = layer["save_index"]
+            y = residual_add(cur, dev[idx])
+            dtype = np.result_type(cur_dtype, outputs[idx].dtype)
+        elif kind == "moe":
+            y, info = moe_forward(cur, layer, variant)
+            layer["_state_aux_loss"] = info["aux_loss"]
+            dtype = cur_dtype
         else:
             raise NotImplementedError(
                 f"layer type {kind!r} is not on enilnets_amd's quantized path")
         spec = layer.get("act_quant")
         if spec is not None:
             y = _fake_quantize_device(y, spec)
-            host = y.numpy().astype(host.dtype, copy=False)
+        if y is cur:
+            host = outputs[-1]
+        else:
+            host = y.numpy()
+            if host.dtype != dtype:
+                host = host.astype(dtype)
         dev.append(y)
         outputs.append(host)
         pre.append(z_host)

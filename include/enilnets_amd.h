@@ -217,6 +217,57 @@ int enq_dense_w8a8(const float* x, int64_t m, int64_t k, const int8_t* codes,
                    int activation, float act_alpha, float act_clip, float* y,
                    int32_t* acc);
 
+/* ---- Transformer-block pieces around the quantized projections -------
+ * LayerNorm over the last axis of an fp32 (rows, cols) matrix:
+ * y = gamma * (x - mean) / sqrt(var + eps) + beta, mean and biased variance
+ * per row.  Replaces layernorm_forward's 2-D / 3-D branches,
+ * Enilnets/nn/forward.py:216-221,240-253 (3-D inputs are (B*S, E) rows). */
+int enq_layernorm(const float* x, int64_t rows, int64_t cols, const float* gamma,
+                  const float* beta, float eps, float* y);
+
+/* y = a + b over n fp32 values (16-byte aligned buffers).  Replaces the
+ * residual_add branch x = x + outputs[save_index], forward.py:762-766. */
+int enq_add(const float* a, const float* b, int64_t n, float* y);
+
+/* Softmax attention core of the multi-head attention layer,
+ * forward.py:431-436,525-549 (absolute positions, softmax kernel):
+ * for batch b, query head h and its K/V head h / (heads / kv_heads)
+ * (_repeat_kv, forward.py:165-171),
+ *   out[b, s, h*D:(h+1)*D] = softmax(q_h k_h^T / sqrt(D) + mask) v_h
+ * with the mask of _window_mask (forward.py:102-117): causal forbids key
+ * j > query i, window >= 0 forbids |i - j| > window (window < 0: none).
+ * q, k, v, out are row-major (batch*seq, ld*) fp32 matrices whose head h
+ * occupies columns [h*D, (h+1)*D); a fused QKV projection output is passed
+ * as three pointers into one buffer with the same row stride.  head_dim is
+ * 16, 32, 64 or 128 (other values: ENQ_ERR_UNSUPPORTED); rows 16-byte
+ * aligned. */
+int enq_attention(const float* q, int64_t ldq, const float* k, int64_t ldk,
+                  const float* v, int64_t ldv, int64_t batch, int64_t seq,
+                  int heads, int kv_heads, int head_dim, int causal,
+                  int64_t window, float* out, int64_t ldo);
+
+/* ---- Mixture of experts on int8 expert weights ------------------------
+ * Replaces moe_forward, Enilnets/nn/moe.py:52-87, for x (tokens, d) fp32:
+ * router logits = x . (wr * sr)^T + br (experts, d) unless router_logits
+ * (tokens, experts) is given; probs = softmax(logits); the top_k experts of
+ * each token by probability (ties: lower expert index first); gates = the
+ * raw probabilities; for each expert e, over its tokens in token order,
+ *   y = act(x . (w1[e] * s1[e])^T + b1[e]) . (w2[e] * s2[e])^T + b2[e]
+ * and out[t] = sum over t's experts in ascending expert index of gate * y.
+ * w1 (experts, hidden, d) and w2 (experts, d, hidden) int8 codes with one
+ * fp32 scale per output row (s1: experts*hidden, s2: experts*d); biases may
+ * be NULL.  Optional outputs: probs (tokens, experts), top_idx (tokens,
+ * top_k) int32 in slot order, aux_loss (one double on the device: the
+ * load-balancing loss of moe.py:38-49).  experts <= 256; softmax is not an
+ * accepted expert activation.  variant as in enq_dense_w8. */
+int enq_moe_w8(const float* x, int64_t tokens, int64_t d, const float* router_logits,
+               const int8_t* wr, const float* sr, const float* br,
+               const int8_t* w1, const float* s1, const float* b1,
+               const int8_t* w2, const float* s2, const float* b2,
+               int64_t experts, int64_t hidden, int top_k,
+               int activation, float act_alpha, float act_clip, int variant,
+               float* out, float* probs, int32_t* top_idx, double* aux_loss);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,12 +18,12 @@ from .quantization import (QUANTIZABLE, compute_scale, dequantize,
                            quantize, quantize_tensor, quantize_weights,
                            int8_codes)
 from .forward import (activate, dense_forward, forward, forward_top_k, layernorm_forward,
-                      mha_forward, moe_forward, router, w8a8_dense)
+                      mha_forward, moe_forward, router, top_k, w8a8_dense, window_mask)
 
 __all__ = [
     "QUANTIZABLE", "compute_scale", "dequantize", "fake_quantize",
     "quant_range", "quantization_error", "quantize", "quantize_tensor",
     "quantize_weights", "int8_codes", "activate", "dense_forward", "forward",
     "layernorm_forward", "mha_forward", "moe_forward", "w8a8_dense", "forward_top_k",
-    "router",
+    "router", "top_k", "window_mask",
 ]

@@ -91,11 +91,25 @@ def layernorm_forward(x: Any, layer: Dict[str, Any]) -> Any:
     return gamma * ((x - mu) / np.sqrt(var + eps)) + beta
 
 
+def window_mask(seq: int, causal: bool, window: Optional[int]) -> Optional[Any]:
+    """Additive attention mask, following ``nn/forward.py:102-117``: -inf
+    where key j may not be seen from query i (causal: j > i; window:
+    |i - j| > window), else 0; None when nothing is masked."""
+    if not causal and window is None:
+        return None
+    pos = np.arange(seq)
+    diff = pos[:, None] - pos[None, :]
+    blocked = diff < 0 if causal else np.zeros(diff.shape, dtype=bool)
+    if window is not None:
+        blocked = blocked | (np.abs(diff) > window)
+    return np.where(blocked, -np.inf, 0.0)
+
+
 def mha_forward(x: Any, layer: Dict[str, Any]) -> Any:
     """Softmax multi-head self-attention with absolute positions.
 
     Follows ``nn/forward.py:423-430`` (projections), ``:525,538-549``
-    (scores, optional causal mask, softmax, context) and ``:550-551``
+    (scores, causal / sliding-window mask, softmax, context) and ``:550-551``
     (output projection).  Grouped K/V heads are expanded group-major as in
     ``forward.py:165-171``."""
     B, S, E = x.shape
@@ -112,10 +126,9 @@ def mha_forward(x: Any, layer: Dict[str, Any]) -> Any:
         kh = np.repeat(kh, H // Hkv, axis=1)
         vh = np.repeat(vh, H // Hkv, axis=1)
     scores = np.matmul(qh, kh.transpose(0, 1, 3, 2)) / np.sqrt(Dh)
-    if layer.get("causal", False):
-        pos = np.arange(S)
-        blocked = (pos[:, None] - pos[None, :]) < 0
-        scores = scores + np.where(blocked, -np.inf, 0.0)[None, None]
+    mask = window_mask(S, layer.get("causal", False), layer.get("window_size"))
+    if mask is not None:
+        scores = scores + mask[None, None]
     m = np.max(scores, axis=-1, keepdims=True)
     e = np.exp(scores - m)
     attn = e / np.sum(e, axis=-1, keepdims=True)

@@ -360,3 +360,88 @@ def test_moe_matches_dense_mixture():
             if e in top:
                 want[t] += p[t, e] * y
     assert np.allclose(got.reshape(-1, 6), want, atol=1e-10, rtol=0)
+
+
+def test_window_mask_matches_definition():
+    # nn/forward.py:102-117 by its definition: key j is hidden from query i
+    # when causal and j > i, or when |i - j| > window.
+    for causal in (False, True):
+        for window in (None, 0, 1, 3):
+            m = oracle.window_mask(7, causal, window)
+            if not causal and window is None:
+                assert m is None
+                continue
+            for i in range(7):
+                for j in range(7):
+                    hidden = (causal and j > i) or (window is not None and abs(i - j) > window)
+                    assert m[i, j] == (-np.inf if hidden else 0.0)
+
+
+def _mha_layer(rng, e=8, h=2, hkv=None, causal=False, window=None):
+    hkv = h if hkv is None else hkv
+    dh = e // h
+    layer = {"type": "multihead_attention", "embed_dim": e, "num_heads": h,
+             "num_kv_heads": hkv, "head_dim": dh, "causal": causal, "window_size": window}
+    for name, rows in (("q", e), ("k", hkv * dh), ("v", hkv * dh), ("o", e)):
+        layer["W" + name] = rng.standard_normal((rows, e)) * 0.4
+        layer["b" + name] = rng.standard_normal(rows) * 0.1
+    return layer
+
+
+def test_mha_matches_explicit_loops():
+    # Per batch, head, query: scores against every allowed key, softmax,
+    # weighted sum of values, in plain Python loops over float64.
+    rng = np.random.default_rng(21)
+    for causal, window, hkv in ((False, None, 2), (True, None, 2), (False, 1, 1), (True, 2, 2)):
+        L = _mha_layer(rng, hkv=hkv, causal=causal, window=window)
+        x = rng.standard_normal((2, 5, 8))
+        got = oracle.mha_forward(x, L)
+        q = x @ L["Wq"].T + L["bq"]
+        k = x @ L["Wk"].T + L["bk"]
+        v = x @ L["Wv"].T + L["bv"]
+        dh, H = L["head_dim"], L["num_heads"]
+        ctx = np.zeros_like(q)
+        for b in range(2):
+            for h in range(H):
+                g = h // (H // hkv)
+                for i in range(5):
+                    keys = [j for j in range(5) if not (causal and j > i)
+                            and not (window is not None and abs(i - j) > window)]
+                    s = np.array([q[b, i, h*dh:(h+1)*dh] @ k[b, j, g*dh:(g+1)*dh]
+                                  for j in keys]) / np.sqrt(dh)
+                    w = np.exp(s - s.max())
+                    w /= w.sum()
+                    ctx[b, i, h*dh:(h+1)*dh] = sum(wj * v[b, j, g*dh:(g+1)*dh]
+                                                   for wj, j in zip(w, keys))
+        want = ctx @ L["Wo"].T + L["bo"]
+        assert np.allclose(got, want, atol=1e-12, rtol=0)
+
+
+def test_mha_window_zero_and_gqa_invariants():
+    # test_enilnets.py:7722-7733 (window 0 reduces to Wo(Wv x)) and
+    # :7557-7573 (GQA equals MHA with group-major repeated K/V weights).
+    rng = np.random.default_rng(22)
+    L = _mha_layer(rng, window=0)
+    x = rng.standard_normal((2, 5, 8))
+    want = (x @ L["Wv"].T + L["bv"]) @ L["Wo"].T + L["bo"]
+    assert np.allclose(oracle.mha_forward(x, L), want, atol=1e-12)
+    g = _mha_layer(rng, h=4, hkv=2)
+    m = dict(g, num_kv_heads=4)
+    for w, b in (("Wk", "bk"), ("Wv", "bv")):
+        m[w] = np.repeat(g[w].reshape(2, 2, 8), 2, axis=0).reshape(8, 8)
+        m[b] = np.repeat(g[b].reshape(2, 2), 2, axis=0).reshape(8)
+    assert np.allclose(oracle.mha_forward(x, g), oracle.mha_forward(x, m), atol=1e-12)
+
+
+def test_layernorm_closed_form():
+    # gamma = 1, beta = 0: every row has mean 0 and variance var/(var+eps);
+    # a constant row maps to beta.
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((4, 3, 16)) * 3 + 1
+    L = {"gamma": np.ones(16), "beta": np.zeros(16), "epsilon": 1e-5}
+    y = oracle.layernorm_forward(x, L)
+    var = x.var(axis=-1)
+    assert np.allclose(y.mean(axis=-1), 0, atol=1e-12)
+    assert np.allclose(y.var(axis=-1), var / (var + 1e-5), atol=1e-12)
+    L2 = {"gamma": np.arange(16.0), "beta": np.full(16, 0.5)}
+    assert np.allclose(oracle.layernorm_forward(np.full((2, 16), 7.0), L2), 0.5)
