@@ -362,11 +362,12 @@ __global__ __launch_bounds__(WM * WN * 64) void w8_gemm_kernel(
 //   A: PLANES x BM rows of 64 bytes (32 bf16), chunks XOR-swizzled (swz64);
 //   B: BN rows of 32 bytes (32 codes), 16-byte halves swapped on bit 3 of the
 //      row, so 16 consecutive rows read at one half hit distinct banks.
+// Each stage's codes are expanded to bf16 once per workgroup (one 16-code
+// item per thread) into one of two bf16 copies of the B tile (64-byte rows,
+// swz64, the A layout), one stage ahead of the MFMAs that read them.
 // Within a stage lane group g = l / 32 owns k in [16 g, 16 g + 16): the two
-// 32x32x16 MFMA steps take k 16 g + [0, 8) and 16 g + [8, 16), so one 128-bit
-// read gives a lane its 16 codes for the stage (expanded to bf16 in
-// registers), and A fragments are chunks 2 g and 2 g + 1 of the row.  The
-// schedule is the same software pipeline as the W8A8 ring kernel.
+// 32x32x16 MFMA steps take k 16 g + [0, 8) and 16 g + [8, 16), i.e. chunks
+// 2 g and 2 g + 1 of an A or bf16 B row.
 // ---------------------------------------------------------------------------
 template <int BM_, int BN_, int WM_, int WN_, int PLANES_, int STAGES_>
 struct RingCfg {
@@ -377,13 +378,16 @@ struct RingCfg {
   static constexpr int A_BYTES = PLANES * BM * 64;   // bf16 rows of 64 bytes
   static constexpr int B_BYTES = BN * 32;            // code rows of 32 bytes
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int BCONV_BYTES = BN * 64;         // one bf16 copy of a B tile
   static constexpr int A_BLOCKS = A_BYTES / 1024, B_BLOCKS = B_BYTES / 1024;
   static constexpr int BLOCKS = A_BLOCKS + B_BLOCKS;
   // every wave issues the same number of 1 KiB blocks (vmcnt accounting);
   // waves past the last block repeat it, rewriting identical bytes
   static constexpr int DMA_PER_WAVE = (BLOCKS + NT / 64 - 1) / (NT / 64);
   static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole 1 KiB blocks");
-  static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS budget");
+  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES + 2 * BCONV_BYTES;
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  static_assert(NT >= 2 * BN, "one expansion item per thread");
 };
 
 __device__ __forceinline__ int swz32(int row, int half) { return half ^ ((row >> 3) & 1); }
@@ -479,7 +483,11 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   const int lrow = lane & 31, g = lane >> 5;
-  int a_off[PLANES][FM][2], b_off[FN];
+
+  // bf16 copies of the B tiles, double-buffered after the ring: each tile
+  // is expanded once per workgroup instead of once per wave that reads it
+  char* bconv = lds + STAGES * C::STAGE_BYTES;
+  int a_off[PLANES][FM][2], b_off[FN][2];
 #pragma unroll
   for (int p = 0; p < PLANES; ++p)
 #pragma unroll
@@ -492,14 +500,35 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int r = wn * TN + j * 32 + lrow;
-    b_off[j] = C::A_BYTES + r * 32 + 16 * swz32(r, g);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) b_off[j][ks] = r * 64 + 16 * swz64(r, 2 * g + ks);
   }
+  // conversion item of this thread: 16 codes of B row cr, k half ch, which
+  // become logical 16-byte chunks 2 ch and 2 ch + 1 of the bf16 row
+  const bool converts = tid < BN * 2;
+  const int cr = tid >> 1, ch = tid & 1;
+  const int conv_src = C::A_BYTES + cr * 32 + 16 * swz32(cr, ch);
+  const int conv_dst0 = cr * 64 + 16 * swz64(cr, 2 * ch);
+  const int conv_dst1 = cr * 64 + 16 * swz64(cr, 2 * ch + 1);
+  auto convert = [&](int t) {
+    if (!converts) return;
+    const int4 raw =
+        *reinterpret_cast<const int4*>(lds + (t % STAGES) * C::STAGE_BYTES + conv_src);
+    bf16x8 first, second;
+    codes16_to_bf16(raw, first, second);
+    char* dst = bconv + (t & 1) * C::BCONV_BYTES;
+    *reinterpret_cast<bf16x8*>(dst + conv_dst0) = first;
+    *reinterpret_cast<bf16x8*>(dst + conv_dst1) = second;
+  };
   bf16x8 fa[PLANES][FM][2], fb[FN][2];
-  int4 braw[FN];
   auto read_frags = [&](int t) {
     const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
+    const char* bt = bconv + (t & 1) * C::BCONV_BYTES;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) braw[j] = *reinterpret_cast<const int4*>(st + b_off[j]);
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        fb[j][ks] = *reinterpret_cast<const bf16x8*>(bt + b_off[j][ks]);
 #pragma unroll
     for (int p = 0; p < PLANES; ++p)
 #pragma unroll
@@ -508,11 +537,26 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
         for (int ks = 0; ks < 2; ++ks)
           fa[p][i][ks] = *reinterpret_cast<const bf16x8*>(st + a_off[p][i][ks]);
   };
-  auto expand_b = [&]() {
+
 #pragma unroll
-    for (int j = 0; j < FN; ++j) codes16_to_bf16(braw[j], fb[j][0], fb[j][1]);
-  };
-  auto mfmas = [&]() {
+  for (int s0 = 0; s0 < STAGES - 1; ++s0)
+    if (s0 < ktiles) issue(s0);
+  wait_stage(0, STAGES - 2);
+  block_barrier();
+  convert(0);
+  wait_lgkmcnt0();
+
+  // Iteration t: once every wave's copy of stage t + 1 has landed and the
+  // expansion of stage t is written, a barrier; then refill the ring slot
+  // stage t - 1 used, read stage t's fragments, expand stage t + 1's codes
+  // into the other bf16 buffer, and run stage t's MFMAs.
+  for (int t = 0; t < ktiles; ++t) {
+    if (t + 1 < ktiles) wait_stage(t + 1, t + STAGES - 2);
+    block_barrier();
+    if (t + STAGES - 1 < ktiles) issue(t + STAGES - 1);
+    read_frags(t);
+    if (t + 1 < ktiles) convert(t + 1);
+    wait_lgkmcnt0();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -522,51 +566,6 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
 #pragma unroll
           for (int p = 0; p < PLANES; ++p)
             acc[i][j] = mfma_32x32x16_bf16(fa[p][i][ks], fb[j][ks], acc[i][j]);
-  };
-
-#pragma unroll
-  for (int s0 = 0; s0 < STAGES - 1; ++s0)
-    if (s0 < ktiles) issue(s0);
-  wait_stage(0, STAGES - 2);
-  wait_lgkmcnt0();
-  block_barrier();
-  read_frags(0);
-
-  // per stage: fragments of t are in registers; wait for stage t + 1, let the
-  // ring advance, read t + 1 while the MFMAs of t run.
-  for (int t = 0; t < ktiles; ++t) {
-    wait_lgkmcnt0();
-    expand_b();
-    bf16x8 ca[PLANES][FM][2], cb[FN][2];
-#pragma unroll
-    for (int p = 0; p < PLANES; ++p)
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        ca[p][i][0] = fa[p][i][0];
-        ca[p][i][1] = fa[p][i][1];
-      }
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      cb[j][0] = fb[j][0];
-      cb[j][1] = fb[j][1];
-    }
-    if (t + 1 < ktiles) {
-      wait_stage(t + 1, t + STAGES - 2);
-      block_barrier();
-      if (t + STAGES - 1 < ktiles) issue(t + STAGES - 1);
-      sched_fence();
-      read_frags(t + 1);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int p = 0; p < PLANES; ++p)
-            acc[i][j] = mfma_32x32x16_bf16(ca[p][i][ks], cb[j][ks], acc[i][j]);
-    sched_fence();
   }
 
   const int lhalf = lane >> 5;
@@ -601,7 +600,7 @@ void launch_w8_ring(const uint16_t* xa, int64_t plane_stride, int64_t kp, const 
   const int64_t tiles_m = ceil_div(m, C::BM) + (grp.offsets ? grp.groups : 0);
   const int64_t tiles_n = ceil_div(n, C::BN);
   ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
-  const size_t lds_bytes = size_t(C::STAGES) * C::STAGE_BYTES;
+  const size_t lds_bytes = size_t(C::LDS_BYTES);
   static bool attr_set = false;
   if (!attr_set) {
     ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8_ring_kernel<C, false>),
@@ -636,8 +635,9 @@ void launch_gemm(const uint16_t* xa, int64_t plane_stride, int64_t kp, const int
 }
 
 // Tile choice: 256 x 256 tiles when they alone fill the device, otherwise
-// 64 x 64 tiles, whose four-fold more workgroups hide latency better than
-// 128 x 128 ones on the MLP shapes (measured 0.134 vs 0.161 ms per step).
+// 128 x 128 tiles with 8 waves.  Measured on the MLP step (0.108 ms vs
+// 0.118 for 64 x 64 tiles), the transformer block (0.671 vs 0.756 ms) and
+// the 4096 x 8192 x 8192 GEMM (1.24 ms for 256 x 256 vs 1.84 ms).
 template <int PLANES, int KMODE>
 void gemm_dispatch(const uint16_t* xa, int64_t plane_stride, int64_t kp, const int8_t* w,
                    int64_t ldw, const float* scale, const float* bias, int64_t m, int64_t n,
@@ -650,8 +650,8 @@ void gemm_dispatch(const uint16_t* xa, int64_t plane_stride, int64_t kp, const i
       launch_w8_ring<RingCfg<256, 256, 4, 2, PLANES, PLANES == 2 ? 3 : 4>>(
           xa, plane_stride, kp, w, scale, bias, m, n, k, ep, y, z, grp);
     else
-      launch_w8_ring<RingCfg<64, 64, 2, 2, PLANES, 4>>(xa, plane_stride, kp, w, scale, bias, m,
-                                                        n, k, ep, y, z, grp);
+      launch_w8_ring<RingCfg<128, 128, 4, 2, PLANES, 4>>(
+          xa, plane_stride, kp, w, scale, bias, m, n, k, ep, y, z, grp);
     return;
   }
   // register-staged kernel: any K, any code alignment; no row groups
