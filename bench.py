@@ -448,7 +448,7 @@ def main():
                                "per-output-channel int8 weights",
                    "global_batch": 4096, "layers": 3, "variant": "fp32",
                    "flops_per_step": flops},
-        "roofline": {"bound": "mfma", "kernel": "w8_gemm_kernel",
+        "roofline": {"bound": "mfma", "kernel": "w8_ring_kernel (+ split_planes_kernel)",
                      "shape": [dom["m"], dom["n"], dom["k"]],
                      "achieved": round(dom_tf, 3), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(dom_tf / BF16_PEAK_TFLOPS, 4),
