@@ -93,52 +93,162 @@ __device__ __forceinline__ int4 load_codes16(const int8_t* __restrict__ w, int64
 }
 
 // ---------------------------------------------------------------------------
-// GEMV (m <= 64): grid (column groups, K splits), 8 waves per block.  Each
-// wave owns a K range of `chunks` x 128 and keeps the activation fragments of
-// that range in registers; it then streams 16-column blocks of W, and the 8
-// waves' partial tiles are summed through LDS.
-// Lane layout per 128-wide K chunk: lane l covers column n = l % 16 and
-// k = 32 * (l / 16) + [0, 32); MFMA i of the chunk uses k offsets 8i..8i+7.
+// Activation fragments straight from fp32: 8 consecutive values of a row
+// (zero outside the matrix), split into bf16 hi (and lo) parts.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void load_row8(const float* __restrict__ x, int64_t row, int64_t m,
+                                          int64_t k, int64_t k0, bool vec, float (&v)[8]) {
+  const float* p = x + row * k + k0;
+  if (row < m && vec && k0 + 8 <= k) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (row < m && k0 + e < k) ? p[e] : 0.0f;
+  }
+}
+
+template <int PLANES>
+__device__ __forceinline__ void split8(const float (&v)[8], Pack8& hi, Pack8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint16_t h = bf16_bits_rne(v[e]);
+    hi.h[e] = h;
+    if (PLANES == 2) lo.h[e] = bf16_bits_rne(v[e] - bf16_to_float(h));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV kernels.  Lane layout per 128-wide K chunk: lane l covers column
+// n = l % 16 and, in lane group g = l / 16, the 16-byte pieces
+// k = 16 g + [0, 16) and 64 + 16 g + [0, 16), so each of the two 128-bit
+// weight loads of a chunk reads 64 contiguous bytes of 16 rows.  MFMA i of
+// the chunk (16x16x32 bf16, x as the A operand) takes k offsets
+// gemv_koff(g, i) + [0, 8).  Both kernels write fp32 partial sums per K
+// slice, part[slice][row][n], which gemv_finish_kernel adds up with the
+// scale, bias and activation.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int gemv_koff(int g, int i) { return 64 * (i >> 1) + 16 * g + 8 * (i & 1); }
+
 constexpr int kGemvWaves = 8;
 constexpr int kGemvChunk = 128;
 // outputs this narrow go through the GEMV even for many rows: a GEMM tile
 // grid over them has too few workgroups to stream the activations
 constexpr int64_t kSkinnyN = 32;
 
-template <int MB, int PLANES, int CHUNKS, int KMODE>
-__global__ __launch_bounds__(512) void gemv_w8_kernel(
-    const uint16_t* __restrict__ xa, int64_t plane_stride, int64_t kp,
-    const int8_t* __restrict__ w, int64_t ldw, int64_t n, int64_t k, int chunks_per_wave,
-    int col_blocks_per_group, float* __restrict__ part) {
-  __shared__ float red[kGemvWaves][MB * 16][17];
+// Decode GEMV (m <= 64): grid (groups of 8 x 16 columns, K slices of kr).
+// The workgroup splits its activation slice x[0:16 MB, k0:k0+kr] into bf16
+// planes in LDS once (rows padded by 32 bytes against bank conflicts); each wave then owns 16 columns over the whole slice, issues all its
+// weight loads before the first MFMA, and needs no cross-wave sum.
+template <int MB, int PLANES, int KMODE, int CHUNKS>
+__global__ __launch_bounds__(512) void gemv_decode_kernel(const float* __restrict__ x, int64_t m,
+                                                          int64_t k, int vec,
+                                                          const int8_t* __restrict__ w, int64_t n,
+                                                          int kr, float* __restrict__ part) {
+  extern __shared__ __align__(16) uint16_t xs[];
+  constexpr int ROWS = 16 * MB;
+  const int pitch = kr + 16;  // bf16 elements per LDS row
+  const int64_t k0 = int64_t(blockIdx.y) * kr;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int64_t n0 = (int64_t(blockIdx.x) * kGemvWaves + wave) * 16;
+  const bool active = n0 < n;
+  const int64_t wrow = n0 + col < n ? n0 + col : n - 1;
+  const int64_t k_end = k0 + kr < k ? k0 + kr : k;
+  const int nchunks = int((k_end - k0 + kGemvChunk - 1) / kGemvChunk);
+  // the weight loads go out first: they do not depend on the activations,
+  // so their latency overlaps the staging below
+  int4 wc[CHUNKS][2];
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int64_t kc = k0 + int64_t(c) * kGemvChunk + 16 * grp;
+    if (active && c < nchunks) {
+      wc[c][0] = load_codes16<KMODE>(w, k, wrow, kc, k);
+      wc[c][1] = load_codes16<KMODE>(w, k, wrow, kc + 64, k);
+    } else {
+      wc[c][0] = make_int4(0, 0, 0, 0);
+      wc[c][1] = make_int4(0, 0, 0, 0);
+    }
+  }
+  const int groups8 = kr / 8;
+  for (int idx = threadIdx.x; idx < ROWS * groups8; idx += 512) {
+    const int r = idx / groups8, c8 = (idx - r * groups8) * 8;
+    float v[8];
+    load_row8(x, r, m, k, k0 + c8, vec != 0, v);
+    Pack8 hi, lo;
+    split8<PLANES>(v, hi, lo);
+    *reinterpret_cast<Pack8*>(xs + r * pitch + c8) = hi;
+    if (PLANES == 2) *reinterpret_cast<Pack8*>(xs + (ROWS + r) * pitch + c8) = lo;
+  }
+  __syncthreads();
+  if (!active) return;  // no barrier follows
+  floatx4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    if (c >= nchunks) break;
+    bf16x8 wb[4];
+    codes16_to_bf16(wc[c][0], wb[0], wb[1]);
+    codes16_to_bf16(wc[c][1], wb[2], wb[3]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int p = 0; p < PLANES; ++p) {
+          const bf16x8 xf = *reinterpret_cast<const bf16x8*>(
+              xs + (p * ROWS + mb * 16 + col) * pitch + c * kGemvChunk + gemv_koff(grp, i));
+          acc[mb] = mfma_16x16x32_bf16(xf, wb[i], acc[mb]);
+        }
+  }
+  // 16x16 output layout: lane holds column l % 16, rows 4 * (l / 16) + r
+  if (n0 + col < n) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        part[(int64_t(blockIdx.y) * ROWS + mb * 16 + 4 * grp + r) * n + n0 + col] = acc[mb][r];
+  }
+}
+
+// Tall-skinny GEMV (n <= 32, any m): grid (column groups, K splits, 16-row
+// blocks).  Each wave owns a K range of `chunks` x 128 and keeps the
+// activation fragments of its rows in registers, read from fp32 and split
+// there; it then streams 16-column blocks of W, and the 8 waves' partial
+// tiles are summed through LDS.
+template <int PLANES, int KMODE>
+__global__ __launch_bounds__(512) void gemv_skinny_kernel(
+    const float* __restrict__ x, int64_t m, int64_t k, int vec, const int8_t* __restrict__ w,
+    int64_t n, int chunks_per_wave, int col_blocks_per_group, int64_t mp,
+    float* __restrict__ part) {
+  constexpr int CHUNKS = 2;
+  __shared__ float red[kGemvWaves][16][17];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int64_t k_wave0 = (int64_t(blockIdx.y) * kGemvWaves + wave) * chunks_per_wave * kGemvChunk;
-  // blockIdx.z selects a block of MB x 16 activation rows (tall-skinny use)
-  const int64_t row0 = int64_t(blockIdx.z) * (MB * 16);
-  xa += row0 * kp;
+  const int64_t row0 = int64_t(blockIdx.z) * 16;
 
-  // activation fragments for this wave's K range
-  bf16x8 xf[CHUNKS][MB][PLANES][4];
+  bf16x8 xf[CHUNKS][PLANES][4];
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
-    const int64_t kc = k_wave0 + int64_t(c) * kGemvChunk + 32 * grp;
-    const bool live = c < chunks_per_wave && kc < kp;
+    const int64_t kc = k_wave0 + int64_t(c) * kGemvChunk;
+    const bool live = c < chunks_per_wave;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int p = 0; p < PLANES; ++p) {
-        const uint16_t* src = xa + p * plane_stride + int64_t(mb * 16 + col) * kp + kc;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          xf[c][mb][p][i] = live ? *reinterpret_cast<const bf16x8*>(src + 8 * i) : bf16x8{};
-      }
+    for (int i = 0; i < 4; ++i) {
+      float v[8];
+      load_row8(x, live ? row0 + col : m, m, k, kc + gemv_koff(grp, i), vec != 0, v);
+      Pack8 hi, lo;
+      split8<PLANES>(v, hi, lo);
+      xf[c][0][i] = __builtin_bit_cast(bf16x8, hi);
+      if (PLANES == 2) xf[c][PLANES - 1][i] = __builtin_bit_cast(bf16x8, lo);
+    }
   }
 
-  const int64_t mp = int64_t(gridDim.z) * (MB * 16);
   for (int cb = 0; cb < col_blocks_per_group; ++cb) {
     const int64_t n0 = (int64_t(blockIdx.x) * col_blocks_per_group + cb) * 16;
     if (n0 >= n) break;
@@ -146,18 +256,17 @@ __global__ __launch_bounds__(512) void gemv_w8_kernel(
     int4 wc[CHUNKS][2];
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c) {
-      const int64_t kc = k_wave0 + int64_t(c) * kGemvChunk + 32 * grp;
-      if (c < chunks_per_wave && kc < k) {
-        wc[c][0] = load_codes16<KMODE>(w, ldw, row, kc, k);
-        wc[c][1] = load_codes16<KMODE>(w, ldw, row, kc + 16, k);
+      const int64_t kbase = k_wave0 + int64_t(c) * kGemvChunk;
+      const int64_t kc = kbase + 16 * grp;
+      if (c < chunks_per_wave && kbase < k) {
+        wc[c][0] = load_codes16<KMODE>(w, k, row, kc, k);
+        wc[c][1] = load_codes16<KMODE>(w, k, row, kc + 64, k);
       } else {
         wc[c][0] = make_int4(0, 0, 0, 0);
         wc[c][1] = make_int4(0, 0, 0, 0);
       }
     }
-    floatx4 acc[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c) {
       bf16x8 wb[4];
@@ -166,19 +275,13 @@ __global__ __launch_bounds__(512) void gemv_w8_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-          for (int p = 0; p < PLANES; ++p)
-            acc[mb] = mfma_16x16x32_bf16(xf[c][mb][p][i], wb[i], acc[mb]);
+        for (int p = 0; p < PLANES; ++p) acc = mfma_16x16x32_bf16(xf[c][p][i], wb[i], acc);
     }
-    // 16x16 output layout: lane holds column l % 16, rows 4 * (l / 16) + r
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][mb * 16 + 4 * grp + r][col] = acc[mb][r];
+    for (int r = 0; r < 4; ++r) red[wave][4 * grp + r][col] = acc[r];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < MB * 256; idx += 512) {
-      const int mm = idx >> 4, nn = idx & 15;
+    if (threadIdx.x < 256) {
+      const int mm = threadIdx.x >> 4, nn = threadIdx.x & 15;
       float s = 0.f;
 #pragma unroll
       for (int v = 0; v < kGemvWaves; ++v) s += red[v][mm][nn];
@@ -664,66 +767,90 @@ void gemm_dispatch(const uint16_t* xa, int64_t plane_stride, int64_t kp, const i
                                                ep, y, z);
 }
 
-// Launch geometry of the GEMV: K splits, K chunks per wave, 16-column blocks
-// per block group.
+// Launch geometry of a GEMV: grid (groups, splits, m_blocks), the K slice of
+// a split, and the partial-sum buffer it needs.
 struct GemvPlan {
-  int64_t m_blocks;  // grid blocks along M (each MB x 16 rows)
-  int mb;      // 16-row activation blocks (1, 2 or 4)
-  int chunks;  // template bound on K chunks per wave
-  int64_t splits;
-  int chunks_per_wave;
-  int cb_per_group;
-  int64_t groups;
+  bool decode;       // gemv_decode_kernel (m <= 64), else gemv_skinny_kernel
+  int mb;            // decode: 16-row activation blocks (1, 2 or 4)
+  int kr;            // decode: K slice per workgroup (multiple of 128)
+  int chunks_per_wave, cb_per_group;  // skinny
+  int64_t groups, splits, m_blocks, mp;
+  size_t part_bytes(int64_t n) const { return sizeof(float) * size_t(splits * mp * n); }
 };
 
-GemvPlan plan_gemv(int64_t m, int64_t n, int64_t kp) {
-  GemvPlan g;
-  g.mb = m <= 16 ? 1 : (m <= 32 ? 2 : (m <= 64 ? 4 : 1));
-  g.chunks = g.mb == 1 ? 2 : 1;
-  g.m_blocks = ceil_div(m, g.mb * 16);
-  const int64_t chunks_total = ceil_div(kp, kGemvChunk);
-  g.splits = ceil_div(chunks_total, int64_t(kGemvWaves) * g.chunks);
-  g.chunks_per_wave = int(ceil_div(chunks_total, g.splits * kGemvWaves));
-  const int64_t col_blocks = ceil_div(n, 16);
-  // enough column groups to fill the device together with the K splits
-  const int64_t want_groups =
-      std::max<int64_t>(1, (int64_t(device_cu_count()) * 2) / (g.splits * g.m_blocks));
-  int cb = int(std::max<int64_t>(1, col_blocks / want_groups));
-  g.cb_per_group = std::min(cb, 8);
-  g.groups = ceil_div(col_blocks, g.cb_per_group);
+GemvPlan plan_gemv(int64_t m, int64_t n, int64_t k) {
+  GemvPlan g{};
+  const int64_t cus = device_cu_count();
+  if (m <= 64) {
+    g.decode = true;
+    g.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    g.m_blocks = 1;
+    g.mp = 16 * g.mb;
+    g.groups = ceil_div(n, 16 * kGemvWaves);
+    // the longest slice the LDS copy allows (16 MB rows x kr <= 16 x 1024),
+    // shortened until groups x splits fill the device twice over
+    const int64_t kr_max = 1024 / g.mb;
+    const int64_t want_splits = ceil_div(2 * cus, g.groups);
+    int64_t kr = ceil_div(ceil_div(k, want_splits), kGemvChunk) * kGemvChunk;
+    kr = std::max<int64_t>(kGemvChunk, std::min(kr, kr_max));
+    g.kr = int(kr);
+    g.splits = ceil_div(k, kr);
+  } else {
+    g.decode = false;
+    g.mb = 1;
+    g.m_blocks = ceil_div(m, 16);
+    g.mp = 16 * g.m_blocks;
+    const int64_t chunks_total = ceil_div(k, kGemvChunk);
+    g.splits = ceil_div(chunks_total, int64_t(kGemvWaves) * 2);
+    g.chunks_per_wave = int(ceil_div(chunks_total, g.splits * kGemvWaves));
+    const int64_t col_blocks = ceil_div(n, 16);
+    const int64_t want_groups = std::max<int64_t>(1, (2 * cus) / (g.splits * g.m_blocks));
+    g.cb_per_group = int(std::min<int64_t>(8, std::max<int64_t>(1, col_blocks / want_groups)));
+    g.groups = ceil_div(col_blocks, g.cb_per_group);
+  }
   ENQ_REQUIRE(g.groups <= 0x7fffffff && g.splits <= 65535 && g.m_blocks <= 65535,
               "problem too large");
   return g;
 }
 
-template <int MB, int PLANES, int CHUNKS, int KMODE>
-void launch_gemv(const GemvPlan& g, const uint16_t* xa, int64_t plane_stride, int64_t kp,
-                 const int8_t* w, int64_t ldw, const float* scale, const float* bias, int64_t m,
-                 int64_t n, int64_t k, const Epilogue& ep, float* y, float* z, float* part) {
-  const int64_t mp = g.m_blocks * MB * 16;
-  gemv_w8_kernel<MB, PLANES, CHUNKS, KMODE>
-      <<<dim3(unsigned(g.groups), unsigned(g.splits), unsigned(g.m_blocks)), 512, 0, stream()>>>(
-          xa, plane_stride, kp, w, ldw, n, k, g.chunks_per_wave, g.cb_per_group, part);
-  check_launch("gemv_w8_kernel");
-  const int64_t total = m * n;
-  gemv_finish_kernel<<<unsigned(ceil_div(total, 256)), 256, 0, stream()>>>(
-      part, int(g.splits), mp, m, n, scale, bias, ep, y, z);
-  check_launch("gemv_finish_kernel");
+template <int MB, int PLANES, int KMODE>
+void launch_decode(const GemvPlan& g, const float* x, int64_t m, int64_t k, int vec,
+                   const int8_t* w, int64_t n, float* part) {
+  constexpr int CHUNKS = 8 / MB;  // kr <= 1024 / MB
+  const size_t lds = size_t(PLANES) * 16 * MB * (g.kr + 16) * sizeof(uint16_t);
+  auto kernel = gemv_decode_kernel<MB, PLANES, KMODE, CHUNKS>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024));
+    attr_set = true;
+  }
+  kernel<<<dim3(unsigned(g.groups), unsigned(g.splits)), 512, lds, stream()>>>(x, m, k, vec, w, n,
+                                                                            g.kr, part);
+  check_launch("gemv_decode_kernel");
 }
 
 template <int PLANES, int KMODE>
-void gemv_dispatch(const GemvPlan& g, const uint16_t* xa, int64_t plane_stride, int64_t kp,
-                   const int8_t* w, int64_t ldw, const float* scale, const float* bias, int64_t m,
-                   int64_t n, int64_t k, const Epilogue& ep, float* y, float* z, float* part) {
-  if (g.mb == 1)
-    launch_gemv<1, PLANES, 2, KMODE>(g, xa, plane_stride, kp, w, ldw, scale, bias, m, n, k, ep,
-                                     y, z, part);
-  else if (g.mb == 2)
-    launch_gemv<2, PLANES, 1, KMODE>(g, xa, plane_stride, kp, w, ldw, scale, bias, m, n, k, ep,
-                                     y, z, part);
-  else
-    launch_gemv<4, PLANES, 1, KMODE>(g, xa, plane_stride, kp, w, ldw, scale, bias, m, n, k, ep,
-                                     y, z, part);
+void gemv_dispatch(const GemvPlan& g, const float* x, const int8_t* w, const float* scale,
+                   const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep,
+                   float* y, float* z, float* part) {
+  const int vec = (k % 4 == 0) && aligned(x, 16);
+  if (g.decode) {
+    if (g.mb == 1)
+      launch_decode<1, PLANES, KMODE>(g, x, m, k, vec, w, n, part);
+    else if (g.mb == 2)
+      launch_decode<2, PLANES, KMODE>(g, x, m, k, vec, w, n, part);
+    else
+      launch_decode<4, PLANES, KMODE>(g, x, m, k, vec, w, n, part);
+  } else {
+    gemv_skinny_kernel<PLANES, KMODE>
+        <<<dim3(unsigned(g.groups), unsigned(g.splits), unsigned(g.m_blocks)), 512, 0,
+           stream()>>>(x, m, k, vec, w, n, g.chunks_per_wave, g.cb_per_group, g.mp, part);
+    check_launch("gemv_skinny_kernel");
+  }
+  gemv_finish_kernel<<<unsigned(ceil_div(m * n, 256)), 256, 0, stream()>>>(
+      part, int(g.splits), g.mp, m, n, scale, bias, ep, y, z);
+  check_launch("gemv_finish_kernel");
 }
 
 }  // namespace
@@ -777,50 +904,44 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
               int64_t n, const float* bias, const Epilogue& ep, int variant, float* y, float* z) {
   const int planes = variant == ENQ_W8_FP32 ? 2 : 1;
   // split-K GEMV for few activation rows, and for tall-skinny outputs (one
-  // 16-row block per grid z index, so at most 65535 * 16 rows)
+  // 16-row block per grid z index, so at most 65535 * 16 rows); both read
+  // the fp32 activations directly
   const bool gemv = m <= 64 || (n <= kSkinnyN && m <= int64_t(65535) * 16);
-  const int64_t kp = ceil_div(k, gemv ? kGemvChunk : kBK) * (gemv ? kGemvChunk : kBK);
-  GemvPlan plan{};
-  size_t part_bytes = 0;
-  int64_t mp = m;
-  if (gemv) {
-    plan = plan_gemv(m, n, kp);
-    mp = plan.m_blocks * plan.mb * 16;
-    part_bytes = sizeof(float) * size_t(plan.splits) * size_t(mp) * size_t(n);
-  }
-  const int64_t plane_stride = mp * kp;
-  const size_t planes_bytes = ((size_t(planes) * plane_stride * sizeof(uint16_t)) + 255) / 256 * 256;
-  // one allocation for everything this call needs, taken before any launch
-  char* ws = static_cast<char*>(workspace(planes_bytes + part_bytes));
-  auto* xa = reinterpret_cast<uint16_t*>(ws);
-  float* part = reinterpret_cast<float*>(ws + planes_bytes);
-  split_planes(x, nullptr, m, k, xa, mp, kp, planes);
   const int kmode = (k % 32 == 0 && aligned(codes, 16)) ? 0 : ((k % 16 == 0 && aligned(codes, 16)) ? 1 : 2);
-  // the K-split GEMV pads K to 128 and needs chunk guards unless k is a multiple of 128
-  const int gemv_kmode = kmode == 0 ? (k % 128 == 0 ? 0 : 1) : kmode;
-  auto run = [&](auto planes_tag, auto kmode_tag) {
-    constexpr int P = decltype(planes_tag)::value;
-    constexpr int KM = decltype(kmode_tag)::value;
-    if (gemv)
-      gemv_dispatch<P, KM>(plan, xa, plane_stride, kp, codes, k, w_scale, bias, m, n, k, ep, y, z,
-                           part);
-    else
-      gemm_dispatch<P, KM>(xa, plane_stride, kp, codes, k, w_scale, bias, m, n, k, ep, y, z);
-  };
   using P1 = std::integral_constant<int, 1>;
   using P2 = std::integral_constant<int, 2>;
   using K0 = std::integral_constant<int, 0>;
   using K1 = std::integral_constant<int, 1>;
   using K2 = std::integral_constant<int, 2>;
-  const int km = gemv ? gemv_kmode : kmode;
-  if (planes == 2) {
-    if (km == 0) run(P2{}, K0{});
-    else if (km == 1) run(P2{}, K1{});
-    else run(P2{}, K2{});
+  auto with_modes = [&](int km, auto&& run) {
+    if (planes == 2) {
+      if (km == 0) run(P2{}, K0{});
+      else if (km == 1) run(P2{}, K1{});
+      else run(P2{}, K2{});
+    } else {
+      if (km == 0) run(P1{}, K0{});
+      else if (km == 1) run(P1{}, K1{});
+      else run(P1{}, K2{});
+    }
+  };
+  if (gemv) {
+    const GemvPlan plan = plan_gemv(m, n, k);
+    auto* part = static_cast<float*>(workspace(plan.part_bytes(n)));
+    // 128-wide K chunks need per-chunk guards unless k is a multiple of 128
+    const int km = kmode == 0 ? (k % 128 == 0 ? 0 : 1) : kmode;
+    with_modes(km, [&](auto planes_tag, auto kmode_tag) {
+      gemv_dispatch<decltype(planes_tag)::value, decltype(kmode_tag)::value>(
+          plan, x, codes, w_scale, bias, m, n, k, ep, y, z, part);
+    });
   } else {
-    if (km == 0) run(P1{}, K0{});
-    else if (km == 1) run(P1{}, K1{});
-    else run(P1{}, K2{});
+    const int64_t kp = ceil_div(k, kBK) * kBK;
+    const int64_t plane_stride = m * kp;
+    auto* xa = static_cast<uint16_t*>(workspace(size_t(planes) * plane_stride * sizeof(uint16_t)));
+    split_planes(x, nullptr, m, k, xa, m, kp, planes);
+    with_modes(kmode, [&](auto planes_tag, auto kmode_tag) {
+      gemm_dispatch<decltype(planes_tag)::value, decltype(kmode_tag)::value>(
+          xa, plane_stride, kp, codes, k, w_scale, bias, m, n, k, ep, y, z);
+    });
   }
   if (ep.activation == ENQ_ACT_SOFTMAX) softmax_rows(y, m, n);
 }
