@@ -350,203 +350,6 @@ __global__ __launch_bounds__(ring::NT, 1) void w8a8_ring_kernel(
   });
 }
 
-// ---------------------------------------------------------------------------
-// Wide-wave W8A8 kernel: 256 x 256 tile, 4 waves (2 x 2) of 128 x 128 each
-// (16 accumulator blocks of 32 x 32 per wave, half the LDS reads per MFMA of
-// the 8-wave layout), same 4-stage direct-to-LDS ring and swizzle.  LDS reads
-// of the next k-step are interleaved with the MFMAs of the current one.
-// ---------------------------------------------------------------------------
-namespace wide {
-constexpr int BM = 256, BN = 256, BK = 64, STAGES = 4;
-constexpr int WM = 2, WN = 2, NT = WM * WN * 64;
-constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-constexpr int ROWS = BM + BN;
-constexpr int STAGE_BYTES = ROWS * BK;
-constexpr int DMA_PER_WAVE = ROWS / 16 / (NT / 64);  // 8
-}  // namespace wide
-
-template <bool KTAIL>
-__global__ __launch_bounds__(wide::NT, 1) void w8a8_wide_kernel(
-    const int8_t* __restrict__ xq, const float* __restrict__ x_scale,
-    const int8_t* __restrict__ wq, const float* __restrict__ w_scale,
-    const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n,
-    Epilogue ep, float* __restrict__ y, int32_t* __restrict__ acc_out) {
-  using namespace wide;
-  extern __shared__ __align__(16) int8_t lds8[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  int tm, tn;
-  xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
-  const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
-
-  const int8_t* src[DMA_PER_WAVE];
-  int chunk_off[DMA_PER_WAVE];
-#pragma unroll
-  for (int j = 0; j < DMA_PER_WAVE; ++j) {
-    const int r = wave * (DMA_PER_WAVE * 16) + 16 * j + (lane >> 2);
-    chunk_off[j] = 16 * swz64(r, lane & 3);
-    if (r < BM) {
-      int64_t g = m0 + r;
-      g = g < m ? g : m - 1;
-      src[j] = xq + g * k + chunk_off[j];
-    } else {
-      int64_t g = n0 + (r - BM);
-      g = g < n ? g : n - 1;
-      src[j] = wq + g * k + chunk_off[j];
-    }
-  }
-  const int ktiles = int(ceil_div(k, BK));
-  const void* zero = g_zero16;
-  auto issue = [&](int t) {
-    int8_t* dst = lds8 + (t % STAGES) * STAGE_BYTES + wave * DMA_PER_WAVE * 1024;
-    const int64_t k0 = int64_t(t) * BK;
-#pragma unroll
-    for (int j = 0; j < DMA_PER_WAVE; ++j) {
-      const void* s_ptr = src[j] + k0;
-      if (KTAIL && k0 + chunk_off[j] >= k) s_ptr = zero;
-      dma16(s_ptr, dst + j * 1024);
-    }
-  };
-  auto wait_stage = [&](int t, int issued) {
-    const int later = (issued < ktiles - 1 ? issued : ktiles - 1) - t;
-    if (later >= 2)
-      wait_vmcnt<2 * DMA_PER_WAVE>();
-    else if (later == 1)
-      wait_vmcnt<DMA_PER_WAVE>();
-    else
-      wait_vmcnt<0>();
-  };
-
-  intx16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
-
-  const int lrow = lane & 31, lhalf = lane >> 5;
-  int a_off[2][FM], b_off[2][FN];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int r = wm * TM + i * 32 + lrow;
-      a_off[ks][i] = r * BK + 16 * swz64(r, 2 * ks + lhalf);
-    }
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int r = BM + wn * TN + j * 32 + lrow;
-      b_off[ks][j] = r * BK + 16 * swz64(r, 2 * ks + lhalf);
-    }
-  }
-  intx4 fa[2][FM], fb[2][FN];
-  auto read_frags = [&](int t, int ks) {
-    const int8_t* st = lds8 + (t % STAGES) * STAGE_BYTES;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) fa[ks][i] = *reinterpret_cast<const intx4*>(st + a_off[ks][i]);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) fb[ks][j] = *reinterpret_cast<const intx4*>(st + b_off[ks][j]);
-  };
-  auto mfmas = [&](int ks) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mfma_32x32x32_i8(fa[ks][i], fb[ks][j], acc[i][j]);
-  };
-  // 16 MFMAs with the 8 fragment reads of the other k-step between them
-  auto interleave = [&]() {
-#pragma unroll
-    for (int g = 0; g < FM + FN; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-  };
-
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < ktiles) issue(s);
-  wait_stage(0, STAGES - 2);
-  wait_lgkmcnt0();
-  block_barrier();
-  read_frags(0, 0);
-
-  for (int t = 0; t < ktiles; ++t) {
-    wait_lgkmcnt0();
-    sched_fence();
-    read_frags(t, 1);
-    mfmas(0);
-    interleave();
-    sched_fence();
-    wait_lgkmcnt0();
-    if (t + 1 < ktiles) {
-      wait_stage(t + 1, t + STAGES - 2);
-      block_barrier();
-      if (t + STAGES - 1 < ktiles) issue(t + STAGES - 1);
-      sched_fence();
-      read_frags(t + 1, 0);
-      mfmas(1);
-      interleave();
-      sched_fence();
-    } else {
-      mfmas(1);
-    }
-  }
-
-  float xs[FM][16];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * lhalf + (e % 4);
-      xs[i][e] = x_scale[row < m ? row : m - 1];
-    }
-  with_activation(ep, [&](auto act) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t col = n0 + wn * TN + j * 32 + lrow;
-      if (col >= n) continue;
-      const float sw = w_scale[col];
-      const float b = bias ? bias[col] : 0.f;
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * lhalf + (e % 4);
-          if (row < m) {
-            const int32_t a = acc[i][j][e];
-            if (acc_out) acc_out[row * n + col] = a;
-            float v = float(a) * xs[i][e];
-            v = v * sw;
-            if (bias) v = v + b;
-            y[row * n + col] = act(v);
-          }
-        }
-    }
-  });
-}
-
-void launch_w8a8_wide(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws,
-                      const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep,
-                      float* y, int32_t* acc) {
-  using namespace wide;
-  const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
-  ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
-  const size_t lds_bytes = size_t(STAGES) * STAGE_BYTES;
-  static bool attr_set = false;
-  if (!attr_set) {
-    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8a8_wide_kernel<false>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
-    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8a8_wide_kernel<true>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
-    attr_set = true;
-  }
-  auto kernel = (k % BK == 0) ? w8a8_wide_kernel<false> : w8a8_wide_kernel<true>;
-  kernel<<<unsigned(tiles_m * tiles_n), NT, lds_bytes, stream()>>>(
-      xq, xs, wq, ws, bias, m, n, k, int(tiles_m), int(tiles_n), ep, y, acc);
-  check_launch("w8a8_wide_kernel");
-}
-
 void launch_w8a8_ring(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws,
                       const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep,
                       float* y, int32_t* acc) {
@@ -605,16 +408,8 @@ void gemm_w8a8(const int8_t* xq, const float* xs, const int8_t* wq, const float*
                int32_t* acc) {
   const bool al = aligned(xq, 16) && aligned(wq, 16);
   const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256);
-  static const int variant = [] {
-    const char* v = getenv("ENQ_W8A8_KERNEL");
-    return v ? atoi(v) : 0;
-  }();
-  if (k % 16 == 0 && al && big_tiles >= device_cu_count() / 2) {
-    if (variant == 1)
-      launch_w8a8_wide(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
-    else
-      launch_w8a8_ring(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
-  }
+  if (k % 16 == 0 && al && big_tiles >= device_cu_count() / 2)
+    launch_w8a8_ring(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
   else if (k % kBK8 == 0 && al)
     w8a8_dispatch<0>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
   else if (k % 16 == 0 && al)
