@@ -26,6 +26,9 @@ SYMMETRIC = 0
 ASYMMETRIC = 1
 W8_FP32 = 0
 W8_BF16 = 1
+AQ_NONE = 0
+AQ_F32 = 1
+AQ_F64 = 2
 
 ACTIVATIONS = {
     "linear": 0, "relu": 1, "leakyrelu": 2, "elu": 3, "selu": 4, "gelu": 5,
@@ -87,6 +90,10 @@ SIGNATURES = {
                               c_float, _P, _P]),
     "enq_dense_w8a8": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, _P, c_int, c_float,
                                c_float, _P, _P]),
+    "enq_dense_w8_aq": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, _P, c_int, c_float,
+                                c_float, c_int, c_int, c_double, c_double, c_float, c_float,
+                                _P, _P]),
+    "enq_act_quant": (c_int, [_P, c_int64, c_int, c_double, c_double, c_float, c_float, _P]),
     "enq_layernorm": (c_int, [_P, c_int64, c_int64, _P, _P, c_float, _P]),
     "enq_add": (c_int, [_P, _P, c_int64, _P]),
     "enq_attention": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, c_int64, c_int64, c_int,

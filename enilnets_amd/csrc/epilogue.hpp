@@ -12,7 +12,28 @@ struct Epilogue {
   int activation;
   float alpha;  // leakyrelu / elu slope (activations.py:22-27)
   float clip;   // sigmoid / softplus clip (activations.py:36-37)
+  // activation fake-quantization after the activation (forward.py:798-805):
+  // ENQ_AQ_NONE, ENQ_AQ_F32 or ENQ_AQ_F64 (the arithmetic of the spec's dtype)
+  int aq = ENQ_AQ_NONE;
+  double aq_scale = 1.0, aq_zp = 0.0;
+  float aq_qmin = 0.0f, aq_qmax = 0.0f;
 };
+
+// fake_quantize (compression/quantization.py:53-69) of one value with a
+// per-tensor scale and zero point: clip(rint(x / scale + zp), qmin, qmax),
+// then (q - zp) * scale; true division, NaN passes the clip.
+__device__ __forceinline__ float fake_quant(float v, const Epilogue& e) {
+  if (e.aq == ENQ_AQ_F64) {
+    const double q = rint(double(v) / e.aq_scale + e.aq_zp);
+    const double c = q < double(e.aq_qmin) ? double(e.aq_qmin)
+                                            : (q > double(e.aq_qmax) ? double(e.aq_qmax) : q);
+    return float((c - e.aq_zp) * e.aq_scale);
+  }
+  const float s = float(e.aq_scale), zp = float(e.aq_zp);
+  const float q = rintf(__fdiv_rn(v, s) + zp);
+  const float c = q < e.aq_qmin ? e.aq_qmin : (q > e.aq_qmax ? e.aq_qmax : q);
+  return __fmul_rn(c - zp, s);
+}
 
 // activations.py:21-41, one element.  relu keeps -0.0 and NaN as np.maximum
 // does; softmax is a row operation and is applied by a separate kernel.
@@ -56,8 +77,18 @@ __device__ __forceinline__ float activate(float x, const Epilogue& e) {
 // Calls body(f) with f the activation as a callable, so the common
 // activations compile into straight-line epilogues instead of a switch per
 // element.
+// activate, then the fake-quantization when the epilogue has one.
+__device__ __forceinline__ float epilogue_out(float x, const Epilogue& e) {
+  const float a = activate(x, e);
+  return e.aq != ENQ_AQ_NONE ? fake_quant(a, e) : a;
+}
+
 template <class Body>
 __device__ __forceinline__ void with_activation(const Epilogue& ep, Body&& body) {
+  if (ep.aq != ENQ_AQ_NONE) {
+    body([ep](float x) { return epilogue_out(x, ep); });
+    return;
+  }
   switch (ep.activation) {
     case ENQ_ACT_LINEAR:
     case ENQ_ACT_SOFTMAX:
@@ -75,6 +106,22 @@ __device__ __forceinline__ void with_activation(const Epilogue& ep, Body&& body)
 // Row-wise softmax in place over an (m, n) fp32 matrix (activations.py:38-40).
 void softmax_rows(float* y, int64_t m, int64_t n);
 
+// The epilogue a GEMM applies itself: a softmax activation runs afterwards
+// as a row kernel, so its fake-quantization must wait for it.
+inline Epilogue gemm_epilogue(const Epilogue& ep) {
+  Epilogue e = ep;
+  if (e.activation == ENQ_ACT_SOFTMAX) e.aq = ENQ_AQ_NONE;
+  return e;
+}
+
+// Row softmax (if the activation is softmax) and the deferred
+// fake-quantization, after a GEMM that applied gemm_epilogue(ep).
+void finish_rows(float* y, int64_t m, int64_t n, const Epilogue& ep);
+
+// y = fake_quant(x) over n values (in place allowed).
+void act_quant(const float* x, int64_t n, const Epilogue& ep, float* y);
+
 bool valid_activation(int act);
+bool valid_act_quant(int mode, double scale, float qmin, float qmax);
 
 }  // namespace enq

@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void gemv_finish_kernel(const float* __restric
   float v = s * scale[c];
   if (bias) v = v + bias[c];
   if (z) z[idx] = v;
-  y[idx] = activate(v, ep);
+  y[idx] = epilogue_out(v, ep);
 }
 
 // ---------------------------------------------------------------------------
@@ -452,7 +452,7 @@ __global__ __launch_bounds__(WM * WN * 64) void w8_gemm_kernel(
           float v = acc[i][j][e] * s;
           if (bias) v = v + b;
           if (z) z[row * n + col] = v;
-          y[row * n + col] = activate(v, ep);
+          y[row * n + col] = epilogue_out(v, ep);
         }
       }
   }
@@ -901,8 +901,10 @@ void dense_w8_grouped(const uint16_t* xa, int64_t plane_stride, int64_t kp, int 
 }
 
 void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const float* w_scale,
-              int64_t n, const float* bias, const Epilogue& ep, int variant, float* y, float* z) {
+              int64_t n, const float* bias, const Epilogue& ep_all, int variant, float* y,
+              float* z) {
   const int planes = variant == ENQ_W8_FP32 ? 2 : 1;
+  const Epilogue ep = gemm_epilogue(ep_all);
   // split-K GEMV for few activation rows, and for tall-skinny outputs (one
   // 16-row block per grid z index, so at most 65535 * 16 rows); both read
   // the fp32 activations directly
@@ -943,7 +945,7 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
           xa, plane_stride, kp, codes, k, w_scale, bias, m, n, k, ep, y, z);
     });
   }
-  if (ep.activation == ENQ_ACT_SOFTMAX) softmax_rows(y, m, n);
+  finish_rows(y, m, n, ep_all);
 }
 
 }  // namespace enq
@@ -961,6 +963,32 @@ extern "C" int enq_dense_w8(const float* x, int64_t m, int64_t k, const int8_t* 
     ENQ_REQUIRE(valid_activation(activation), "unknown activation code %d", activation);
     ENQ_REQUIRE(variant == ENQ_W8_FP32 || variant == ENQ_W8_BF16, "unknown variant %d", variant);
     Epilogue ep{activation, act_alpha, act_clip};
+    dense_w8(x, m, k, codes, w_scale, n, bias, ep, variant, y, z);
+  });
+}
+
+extern "C" int enq_dense_w8_aq(const float* x, int64_t m, int64_t k, const int8_t* codes,
+                               const float* w_scale, int64_t n, const float* bias, int activation,
+                               float act_alpha, float act_clip, int variant, int aq_mode,
+                               double aq_scale, double aq_zero_point, float aq_qmin,
+                               float aq_qmax, float* y, float* z) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && n >= 1 && k >= 1, "m, n, k must be positive (m=%lld n=%lld k=%lld)",
+                (long long)m, (long long)n, (long long)k);
+    ENQ_REQUIRE(x && codes && w_scale && y, "NULL pointer argument");
+    ENQ_REQUIRE(valid_activation(activation), "unknown activation code %d", activation);
+    ENQ_REQUIRE(variant == ENQ_W8_FP32 || variant == ENQ_W8_BF16, "unknown variant %d", variant);
+    ENQ_REQUIRE(aq_mode == ENQ_AQ_F32 || aq_mode == ENQ_AQ_F64, "unknown act-quant mode %d",
+                aq_mode);
+    ENQ_REQUIRE(valid_act_quant(aq_mode, aq_scale, aq_qmin, aq_qmax),
+                "invalid act-quant parameters");
+    Epilogue ep{activation, act_alpha, act_clip};
+    ep.aq = aq_mode;
+    ep.aq_scale = aq_scale;
+    ep.aq_zp = aq_zero_point;
+    ep.aq_qmin = aq_qmin;
+    ep.aq_qmax = aq_qmax;
     dense_w8(x, m, k, codes, w_scale, n, bias, ep, variant, y, z);
   });
 }

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(WM * WN * 64) void w8a8_gemm_kernel(
           float v = float(a) * x_scale[row];
           v = v * sw;
           if (bias) v = v + b;
-          y[row * n + col] = activate(v, ep);
+          y[row * n + col] = epilogue_out(v, ep);
         }
       }
   }
@@ -416,7 +416,7 @@ void gemm_w8a8(const int8_t* xq, const float* xs, const int8_t* wq, const float*
     w8a8_dispatch<1>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
   else
     w8a8_dispatch<2>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
-  if (ep.activation == ENQ_ACT_SOFTMAX) softmax_rows(y, m, n);
+  finish_rows(y, m, n, ep);
 }
 
 }  // namespace enq

@@ -37,6 +37,34 @@ def activation_args(name: str, params: Optional[Dict[str, Any]] = None) -> Tuple
     return _lib.ACTIVATIONS[name], float(alpha), float(clip)
 
 
+def act_quant_args(spec: Dict[str, Any], out_dtype: Any = np.float32) -> Tuple[Any, ...]:
+    """``(mode, scale, zero_point, qmin, qmax, result_dtype)`` of an
+    ``act_quant`` spec (``forward.py:798-805``) applied to a layer output of
+    host dtype ``out_dtype``.  The arithmetic is the dtype NumPy gives
+    ``x / scale + zero_point`` (the calibrator's float64 0-d scale makes it
+    float64 even for float32 outputs)."""
+    from ..compression.quantization import _probe, quant_range
+    qmin, qmax = quant_range(spec["bits"], spec["scheme"])
+    scale, zp = spec["scale"], spec["zero_point"]
+    if np.size(scale) != 1 or np.size(zp) != 1:
+        raise NotImplementedError("act_quant specs are per tensor on the quantized path")
+    res = (np.ones(1, dtype=out_dtype) / _probe(scale) + _probe(zp)).dtype
+    if res not in (np.float32, np.float64):
+        raise NotImplementedError(f"act_quant arithmetic in {res} is not supported")
+    mode = _lib.AQ_F64 if res == np.float64 else _lib.AQ_F32
+    return (mode, float(np.asarray(scale).reshape(-1)[0]), float(np.asarray(zp).reshape(-1)[0]),
+            float(qmin), float(qmax), res)
+
+
+def act_quant(x: DeviceArray, spec: Dict[str, Any], out_dtype: Any = np.float32,
+              out: Optional[DeviceArray] = None) -> DeviceArray:
+    """The standalone fake-quantization pass of a layer output."""
+    mode, scale, zp, qmin, qmax, _ = act_quant_args(spec, out_dtype)
+    y = out if out is not None else DeviceArray(x.shape, np.float32)
+    _lib.call("enq_act_quant", x.ptr, x.size, mode, scale, zp, qmin, qmax, y.ptr)
+    return y
+
+
 def _rows(x: DeviceArray) -> Tuple[int, int]:
     k = x.shape[-1]
     return x.size // max(k, 1), k
@@ -45,9 +73,13 @@ def _rows(x: DeviceArray) -> Tuple[int, int]:
 def dense_w8(x: DeviceArray, w: Int8Weights, bias: Optional[DeviceArray] = None,
              activation: str = "linear", activation_params: Optional[Dict[str, Any]] = None,
              variant: str = "fp32", out: Optional[DeviceArray] = None,
-             pre_activation: Optional[DeviceArray] = None) -> DeviceArray:
+             pre_activation: Optional[DeviceArray] = None,
+             act_quant: Optional[Dict[str, Any]] = None,
+             out_dtype: Any = np.float32) -> DeviceArray:
     """``act(x @ (codes * scale).T + bias)`` for fp32 ``x`` of shape
-    ``(..., k)`` and int8 weights ``(n, k)``."""
+    ``(..., k)`` and int8 weights ``(n, k)``.  ``act_quant`` (a layer's
+    calibrated spec) fake-quantizes the output in the same epilogue, in the
+    arithmetic NumPy uses for an output of host dtype ``out_dtype``."""
     if x.dtype != np.float32:
         raise NotImplementedError(f"W8 Dense takes float32 activations, got {x.dtype}")
     m, k = _rows(x)
@@ -59,9 +91,15 @@ def dense_w8(x: DeviceArray, w: Int8Weights, bias: Optional[DeviceArray] = None,
     code, alpha, clip = activation_args(activation, activation_params)
     out_shape = x.shape[:-1] + (n,)
     y = out if out is not None else DeviceArray(out_shape, np.float32)
-    _lib.call("enq_dense_w8", x.ptr, m, k, w.codes.ptr, w.scale.ptr, n,
-              bias.ptr if bias is not None else null(), code, alpha, clip, VARIANTS[variant],
-              y.ptr, pre_activation.ptr if pre_activation is not None else null())
+    z = pre_activation.ptr if pre_activation is not None else null()
+    b = bias.ptr if bias is not None else null()
+    if act_quant is None:
+        _lib.call("enq_dense_w8", x.ptr, m, k, w.codes.ptr, w.scale.ptr, n, b, code, alpha, clip,
+                  VARIANTS[variant], y.ptr, z)
+    else:
+        mode, scale, zp, qmin, qmax, _ = act_quant_args(act_quant, out_dtype)
+        _lib.call("enq_dense_w8_aq", x.ptr, m, k, w.codes.ptr, w.scale.ptr, n, b, code, alpha,
+                  clip, VARIANTS[variant], mode, scale, zp, qmin, qmax, y.ptr, z)
     return y
 
 

@@ -14,9 +14,8 @@ from typing import Any, Dict, List, Optional
 
 import numpy as np
 
-from .. import _lib
 from ..device import DeviceArray
-from .dense import dense_w8
+from .dense import act_quant, act_quant_args, dense_w8
 from .moe import moe_forward
 from .transformer import layernorm, mha_forward, residual_add
 from .weights import int8_weights
@@ -34,30 +33,15 @@ def _bias(layer: Dict[str, Any], key: str, n: int) -> DeviceArray:
     return DeviceArray.from_numpy(np.ascontiguousarray(b, dtype=np.float32))
 
 
-def _fake_quantize_device(x: DeviceArray, spec: Dict[str, Any]) -> DeviceArray:
-    """``act_quant`` (``forward.py:798-805``): per-tensor fake quantization
-    of a layer output with the calibrated scale and zero point."""
-    from ..compression.quantization import quant_range
-    qmin, qmax = quant_range(spec["bits"], spec["scheme"])
-    scale = np.asarray(spec["scale"])
-    zp = np.asarray(spec["zero_point"])
-    if scale.size != 1 or zp.size != 1:
-        raise NotImplementedError("act_quant specs are per tensor")
-    d_s = DeviceArray.from_numpy(scale.reshape(1).astype(np.float32))
-    d_z = DeviceArray.from_numpy(zp.reshape(1).astype(np.float32))
-    out = DeviceArray(x.shape, np.float32)
-    _lib.call("enq_fake_quantize", _lib.F32, x.ptr, 1, 1, x.size, d_s.ptr, d_z.ptr, qmin, qmax,
-              out.ptr)
-    return out
-
-
 def _dense(cur: DeviceArray, layer: Dict[str, Any], variant: str):
+    """Dense layer; a calibrated ``act_quant`` runs in the GEMM epilogue."""
     w = int8_weights(layer, "weights")
     n = w.shape[0]
     z = DeviceArray(cur.shape[:-1] + (n,), np.float32)
-    y = dense_w8(cur, w, _bias(layer, "bias", n), layer["activation"],
-                 layer.get("activation_params", {}), variant, pre_activation=z)
     dtype = np.float64 if layer["activation"] in _FLOAT64_ACTIVATIONS else np.float32
+    y = dense_w8(cur, w, _bias(layer, "bias", n), layer["activation"],
+                 layer.get("activation_params", {}), variant, pre_activation=z,
+                 act_quant=layer.get("act_quant"), out_dtype=dtype)
     return y, z, dtype
 
 
@@ -110,7 +94,9 @@ def Forward(model: Any, inputs: Any, training: bool = False, dropout_rate: float
                 f"layer type {kind!r} is not on enilnets_amd's quantized path")
         spec = layer.get("act_quant")
         if spec is not None:
-            y = _fake_quantize_device(y, spec)
+            if kind not in ("dense", "sparse"):  # a Dense epilogue applied it already
+                y = act_quant(y, spec, dtype)
+            dtype = act_quant_args(spec, dtype)[-1]
         if y is cur:
             host = outputs[-1]
         else:

@@ -64,6 +64,12 @@ extern "C" {
 #define ENQ_ACT_SOFTMAX 11
 
 /* W8 Dense arithmetic variants */
+/* activation fake-quantization arithmetic (the dtype of the spec's scale
+ * and zero point as NumPy promotes them with float32 outputs) */
+#define ENQ_AQ_NONE 0
+#define ENQ_AQ_F32 1
+#define ENQ_AQ_F64 2
+
 #define ENQ_W8_FP32 0 /* fp32-accurate: activations split into bf16 hi+lo   */
 #define ENQ_W8_BF16 1 /* activations rounded to bf16 once                    */
 
@@ -196,6 +202,24 @@ int enq_dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes,
                  const float* w_scale, int64_t n, const float* bias,
                  int activation, float act_alpha, float act_clip, int variant,
                  float* y, float* z);
+
+/* enq_dense_w8 followed, in the same epilogue, by the activation
+ * fake-quantization of forward.py:798-805 (act_quant spec of a calibrated
+ * layer, compression/quantization.py:156-209):
+ *   y = (clip(rint(act(z) / aq_scale + aq_zero_point), qmin, qmax)
+ *        - aq_zero_point) * aq_scale
+ * in float64 (aq_mode ENQ_AQ_F64: the calibrator's float64 scale promotes the
+ * expression) or float32 (ENQ_AQ_F32), stored as float32.  z is unaffected. */
+int enq_dense_w8_aq(const float* x, int64_t m, int64_t k, const int8_t* codes,
+                    const float* w_scale, int64_t n, const float* bias,
+                    int activation, float act_alpha, float act_clip, int variant,
+                    int aq_mode, double aq_scale, double aq_zero_point,
+                    float aq_qmin, float aq_qmax, float* y, float* z);
+
+/* The same fake-quantization as a standalone pass over n values (for layer
+ * outputs no Dense epilogue produces); y may equal x. */
+int enq_act_quant(const float* x, int64_t n, int mode, double scale, double zero_point,
+                  float qmin, float qmax, float* y);
 
 /* W8A8: int8 activation codes (m, k) with one fp32 scale per row, int8
  * weight codes (n, k) with one fp32 scale per row of W.

@@ -1,0 +1,110 @@
+"""GPU parity of activation fake-quantization (``act_quant``,
+``Enilnets/nn/forward.py:798-805``; specs from ``ActivationCalibrator``,
+``compression/quantization.py:156-209``).
+
+* The standalone pass is bit-identical to the oracle's ``fake_quantize`` in
+  the arithmetic NumPy picks (float64 for the calibrator's float64 scale,
+  float32 for float32 specs), rounded to float32.
+* The Dense epilogue that fuses it is bit-identical to the unfused Dense
+  followed by the standalone pass, on the GEMV and both GEMM tile paths and
+  after a softmax.
+* ``Forward`` with calibrated specs matches the oracle's ``forward``: the
+  layer GEMMs are not bit-exact, so an output may land on the neighbouring
+  grid point (about 2 x 1e-5 x 255 = 0.5% of outputs for an 8-bit grid);
+  every element is within one quantization step and fewer than 2% differ
+  beyond float32 rounding.
+"""
+
+import numpy as np
+import pytest
+
+import enilnets_amd as ea
+from enilnets_amd.device import DeviceArray
+from enilnets_amd.nn import Model
+from enilnets_amd.nn import dense as D
+from enilnets_amd.nn.weights import Int8Weights
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def spec_for(x, bits=8, scheme="asymmetric", dtype=np.float64):
+    low, high = float(np.min(x)), float(np.max(x))
+    scale, zp = oracle.compute_scale(np.asarray(low, dtype), np.asarray(high, dtype), bits, scheme)
+    return {"bits": bits, "scheme": scheme, "scale": scale, "zero_point": zp}
+
+
+@pytest.mark.parametrize("dtype,scheme,bits", [(np.float64, "asymmetric", 8),
+                                               (np.float32, "asymmetric", 8),
+                                               (np.float64, "symmetric", 8),
+                                               (np.float64, "asymmetric", 4)])
+def test_standalone_pass_bit_exact(gpu, dtype, scheme, bits):
+    rng = np.random.default_rng(bits)
+    x = (rng.standard_normal(100003) * 3).astype(np.float32)
+    x[:5] = [0.0, -0.0, np.nan, 1e30, -1e30]
+    spec = spec_for(x[5:], bits, scheme, dtype)
+    want = oracle.fake_quantize(x, spec["scale"], spec["zero_point"], bits, scheme)
+    assert want.dtype == np.result_type(np.float32, dtype)
+    got = D.act_quant(DeviceArray.from_numpy(x), spec).numpy()
+    w32 = want.astype(np.float32)
+    nan = np.isnan(w32)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), w32[~nan].view(np.uint32))
+
+
+def make_w(rng, n, k):
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    fq, scale, _ = oracle.quantize_tensor(w, 8, per_channel=True)
+    codes = oracle.quantize(w, scale, np.zeros_like(scale), 8, "symmetric").astype(np.int8)
+    rows = np.ascontiguousarray(scale.reshape(-1).astype(np.float32))
+    return Int8Weights(DeviceArray.from_numpy(codes), DeviceArray.from_numpy(rows), codes.shape,
+                       8, True, None, None)
+
+
+@pytest.mark.parametrize("m,k,n,act", [(8, 512, 300, "relu"), (4096, 1024, 10, "linear"),
+                                       (300, 784, 1024, "gelu"), (2048, 1024, 4096, "relu"),
+                                       (100, 64, 37, "softmax"), (65, 96, 130, "sigmoid")])
+def test_fused_epilogue_equals_separate_pass(gpu, m, k, n, act):
+    print(f"[case] dense_w8_aq m={m} k={k} n={n} act={act}", flush=True)
+    rng = np.random.default_rng(m + n)
+    w = make_w(rng, n, k)
+    x = DeviceArray.from_numpy(rng.standard_normal((m, k)).astype(np.float32))
+    b = DeviceArray.from_numpy((rng.standard_normal(n) * 0.1).astype(np.float32))
+    plain = D.dense_w8(x, w, b, act)
+    spec = spec_for(plain.numpy())
+    out_dtype = np.float64 if act == "gelu" else np.float32
+    fused = D.dense_w8(x, w, b, act, act_quant=spec, out_dtype=out_dtype).numpy()
+    separate = D.act_quant(plain, spec, out_dtype).numpy()
+    assert np.array_equal(fused.view(np.uint32), separate.view(np.uint32))
+
+
+def test_forward_with_calibrated_activations(gpu):
+    rng = np.random.default_rng(31)
+    m = Model()
+    m.add_dense((rng.standard_normal((256, 100)) * 0.1).astype(np.float32),
+                (rng.standard_normal(256) * 0.01).astype(np.float32), "relu")
+    m.add_dense((rng.standard_normal((128, 256)) * 0.1).astype(np.float32),
+                (rng.standard_normal(128) * 0.01).astype(np.float32), "gelu")
+    m.add_dense((rng.standard_normal((10, 128)) * 0.1).astype(np.float32),
+                (rng.standard_normal(10) * 0.01).astype(np.float32), "linear")
+    ea.quantize_weights(m, per_channel=True)
+    x = rng.uniform(0, 1, (512, 100)).astype(np.float32)
+    cal = ea.ActivationCalibrator(m)
+    cal.observe(x)
+    installed = cal.apply()
+    assert sorted(installed) == [0, 1, 2]
+    m.Forward(x)
+    want = oracle.forward(m.layers, x, dtype=np.float32)
+    for i in range(1, 4):
+        g, w_ = m.outputs[i], want[i]
+        assert g.dtype == w_.dtype, (i, g.dtype, w_.dtype)
+        step = float(m.layers[i - 1]["act_quant"]["scale"])
+        diff = np.abs(g.astype(np.float64) - w_.astype(np.float64))
+        assert np.all(diff <= 1.0001 * step), f"layer {i}: {diff.max()} > {step}"
+        # a pre-quantization value within the GEMM's ~1e-5 relative error of a
+        # rounding boundary may round the other way: about 2 * 1e-5 * 255
+        # grid steps = 0.5% of outputs, a little more after a flipped input
+        off = diff > 1e-6 * np.max(np.abs(w_))
+        assert off.mean() < 2e-2, f"layer {i}: {off.mean():.2e} of outputs off the oracle's grid point"
+    ea.remove_activation_quantization(m)
+    assert all("act_quant" not in L for L in m.layers)
