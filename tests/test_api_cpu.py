@@ -116,3 +116,37 @@ def test_activation_args():
     assert activation_args("leakyrelu", {"alpha": 0.2})[1] == pytest.approx(0.2)
     with pytest.raises(ValueError):
         activation_args("bogus")
+
+
+def test_int8_file_round_trips_unquantized_layers(tmp_path):
+    # no int8 weights: no device needed; every value, dtype and key order back
+    from enilnets_amd.nn import LoadInt8, Model, SaveInt8
+    m = Model()
+    m.add_dense(np.arange(12, dtype=np.float32).reshape(3, 4), activation="relu")
+    m.add_layernorm(3, epsilon=1e-6)
+    m.layers[0]["act_quant"] = {"bits": 8, "scheme": "asymmetric", "scale": np.asarray(0.5),
+                                "zero_point": np.float64(3.0), "low": -1.0, "high": 2.0}
+    m.layers[1]["_state_scratch"] = np.zeros(2)
+    f = tmp_path / "model.int8"
+    info = SaveInt8(m, str(f))
+    assert info == {"int8_bytes": 0, "float_bytes": 0}
+    m2 = LoadInt8(str(f))
+    assert list(m2.layers[0]) == list(m.layers[0])
+    assert "_state_scratch" not in m2.layers[1]
+    for a, b in zip(m.layers, m2.layers):
+        for k, v in b.items():
+            if isinstance(v, np.ndarray):
+                assert v.dtype == a[k].dtype and np.array_equal(v, a[k])
+    aq = m2.layers[0]["act_quant"]
+    assert type(aq["scale"]) is np.ndarray and aq["scale"].dtype == np.float64
+    assert type(aq["zero_point"]) is np.float64 and aq["low"] == -1.0
+
+
+def test_int8_file_rejects_other_archives(tmp_path):
+    from enilnets_amd.nn import LoadInt8
+    f = tmp_path / "other.npz"
+    meta = np.frombuffer(b'{"format": "something-else", "version": 1}', dtype=np.uint8)
+    with open(f, "wb") as fh:
+        np.savez(fh, meta=meta)
+    with pytest.raises(ValueError):
+        LoadInt8(str(f))
