@@ -98,6 +98,12 @@ SIGNATURES = {
     "enq_add": (c_int, [_P, _P, c_int64, _P]),
     "enq_attention": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, c_int64, c_int64, c_int,
                               c_int, c_int, c_int, c_int64, _P, c_int64]),
+    "enq_attention_kv": (c_int, [_P, c_int64, c_int64, c_int64, c_int64, _P, c_int64, _P,
+                                 c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_int,
+                                 c_int, c_int, c_int64, _P, c_int64]),
+    "enq_add_bcast": (c_int, [_P, _P, c_int64, c_int64, _P]),
+    "enq_copy_rows": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64,
+                              c_int64]),
     "enq_moe_w8": (c_int, [_P, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                            c_int64, c_int64, c_int, c_int, c_float, c_float, c_int, _P, _P, _P,
                            _P]),

@@ -10,6 +10,7 @@
 // running max and the rescale follow; then O^T += V^T . P^T reuses the score
 // registers directly as the B operand.  Everything is fp32: products are
 // exact fp32 products, sums fp32.
+#include <algorithm>
 #include <cmath>
 
 #include "common.hpp"
@@ -101,6 +102,41 @@ __global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a,
   }
 }
 
+// y[o, i] = a[o, i] + b[i]: a positional table slice added to every batch row
+// block (forward.py:597-603).
+__global__ __launch_bounds__(256) void add_bcast_kernel(const float* __restrict__ a,
+                                                        const float* __restrict__ b,
+                                                        int64_t outer, int64_t inner,
+                                                        float* __restrict__ y) {
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < outer * inner;
+       i += int64_t(gridDim.x) * 256)
+    y[i] = a[i] + b[i % inner];
+}
+
+// Strided row copy, batch by batch: dst row b * dst_bstride + r (pitch
+// ld_dst) <- src row b * src_bstride + r (pitch ld_src), `width` values.
+// Appends new keys / values to a KV cache and gathers embedding rows
+// (rows == nullptr: identity; else src row rows[r]).
+__global__ __launch_bounds__(256) void copy_rows_kernel(const float* __restrict__ src,
+                                                        int64_t ld_src, int64_t src_bstride,
+                                                        const int* __restrict__ rows,
+                                                        float* __restrict__ dst, int64_t ld_dst,
+                                                        int64_t dst_bstride, int64_t nrows,
+                                                        int64_t width, int64_t batch) {
+  const int64_t total = batch * nrows * width;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * 256) {
+    const int64_t c = i % width, br = i / width;
+    const int64_t r = br % nrows, b = br / nrows;
+    const int64_t sr = rows ? int64_t(rows[b * nrows + r]) : r;
+    dst[(b * dst_bstride + r) * ld_dst + c] = src[(b * src_bstride + sr) * ld_src + c];
+  }
+}
+
+unsigned stride_grid(int64_t work) {
+  return unsigned(std::min<int64_t>(ceil_div(work, 256), int64_t(device_cu_count()) * 32));
+}
+
 // ---------------------------------------------------------------------------
 // Attention core
 // ---------------------------------------------------------------------------
@@ -108,10 +144,16 @@ __device__ __forceinline__ floatx4 mfma_16x16x4_f32(float a, float b, floatx4 c)
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Queries of batch b are rows b * q_bstride + [0, seq_q) of q and out, keys
+// and values rows b * kv_bstride + [0, seq_k) of k and v; query i sits at
+// absolute position q_pos0 + i and key j at k_pos0 + j (a KV cache's keys
+// precede the step's queries).
 struct AttnShape {
-  int64_t batch, seq;
+  int64_t batch, seq_q, seq_k;
   int heads, kv_heads;
   int64_t ldq, ldk, ldv, ldo;  // row strides (elements)
+  int64_t q_bstride, kv_bstride;
+  int64_t q_pos0, k_pos0;
   float scale;                 // 1 / sqrt(head_dim)
   int causal;
   int64_t window;              // < 0: unbounded
@@ -139,10 +181,11 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
   const int kvh = h / (sh.heads / sh.kv_heads);
   const int64_t qblk0 = int64_t(blockIdx.x) * kAttnQ;
   const int64_t qi = qblk0 + wave * 16 + col;  // this lane's query
-  const int64_t S = sh.seq;
-  const float* qb = q + (b * S) * sh.ldq + int64_t(h) * DH;
-  const float* kb = k + (b * S) * sh.ldk + int64_t(kvh) * DH;
-  const float* vb = v + (b * S) * sh.ldv + int64_t(kvh) * DH;
+  const int64_t S = sh.seq_q, SK = sh.seq_k;
+  const int64_t qpos = sh.q_pos0 + qi;         // absolute positions
+  const float* qb = q + (b * sh.q_bstride) * sh.ldq + int64_t(h) * DH;
+  const float* kb = k + (b * sh.kv_bstride) * sh.ldk + int64_t(kvh) * DH;
+  const float* vb = v + (b * sh.kv_bstride) * sh.ldv + int64_t(kvh) * DH;
 
   // Q^T operand: step st of lane group g uses dim g * DG + st.
   float qreg[DG];
@@ -166,12 +209,16 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
   float l_part = 0.0f;      // this lane's share of the running sum
 
   // key blocks that can hold an allowed key for any query of the workgroup
+  // (key indices j, positions k_pos0 + j)
   const int64_t q_last = (qblk0 + kAttnQ - 1 < S - 1) ? qblk0 + kAttnQ - 1 : S - 1;
-  int64_t key_end = S;
-  if (sh.causal) key_end = q_last + 1;
-  if (sh.window >= 0 && q_last + sh.window + 1 < key_end) key_end = q_last + sh.window + 1;
+  const int64_t rel_last = sh.q_pos0 + q_last - sh.k_pos0;  // newest query, in key index
+  const int64_t rel_first = sh.q_pos0 + qblk0 - sh.k_pos0;  // oldest query, in key index
+  int64_t key_end = SK;
+  if (sh.causal && rel_last + 1 < key_end) key_end = rel_last + 1;
+  if (sh.window >= 0 && rel_last + sh.window + 1 < key_end) key_end = rel_last + sh.window + 1;
   int64_t key_begin = 0;
-  if (sh.window >= 0 && qblk0 - sh.window > 0) key_begin = qblk0 - sh.window;
+  if (sh.window >= 0 && rel_first - sh.window > 0) key_begin = rel_first - sh.window;
+  if (key_end < 0) key_end = 0;
   const int64_t kb_begin = key_begin / kAttnKB;
   const int64_t kb_end = (key_end + kAttnKB - 1) / kAttnKB;
 
@@ -184,7 +231,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
       const int r = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
       const int64_t key = key0 + r;
       float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-      if (key < S) {
+      if (key < SK) {
         kv = *reinterpret_cast<const float4*>(kb + key * sh.ldk + c4);
         vv = *reinterpret_cast<const float4*>(vb + key * sh.ldv + c4);
       }
@@ -215,10 +262,11 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t key = key0 + ks * 16 + 4 * grp + i;
-        bool blocked = key >= S;
-        if (sh.causal) blocked = blocked || key > qi;
+        const int64_t kpos = sh.k_pos0 + key;
+        bool blocked = key >= SK;
+        if (sh.causal) blocked = blocked || kpos > qpos;
         if (sh.window >= 0) {
-          const int64_t dlt = qi - key;
+          const int64_t dlt = qpos - kpos;
           blocked = blocked || (dlt > sh.window || -dlt > sh.window);
         }
         const float val = blocked ? -INFINITY : s[ks][i] * sh.scale;
@@ -269,14 +317,14 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
     const int r = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
     const int64_t qq = qblk0 + wave * 16 + r;
     if (qq < S)
-      *reinterpret_cast<float4*>(out + (b * S + qq) * sh.ldo + int64_t(h) * DH + c4) =
+      *reinterpret_cast<float4*>(out + (b * sh.q_bstride + qq) * sh.ldo + int64_t(h) * DH + c4) =
           *reinterpret_cast<const float4*>(&my[r * PITCH + c4]);
   }
 }
 
 void attention(const float* q, const float* k, const float* v, const AttnShape& sh, int head_dim,
                float* out) {
-  const dim3 grid(unsigned(ceil_div(sh.seq, kAttnQ)), unsigned(sh.heads), unsigned(sh.batch));
+  const dim3 grid(unsigned(ceil_div(sh.seq_q, kAttnQ)), unsigned(sh.heads), unsigned(sh.batch));
   switch (head_dim) {
     case 16:
       attention_kernel<16><<<grid, 256, 0, stream()>>>(q, k, v, sh, out);
@@ -341,27 +389,83 @@ extern "C" int enq_add(const float* a, const float* b, int64_t n, float* y) {
   });
 }
 
+namespace {
+
+void check_attention(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                     int64_t ldv, int64_t batch, int heads, int kv_heads, int head_dim,
+                     const float* out, int64_t ldo) {
+  ENQ_REQUIRE(batch >= 1 && heads >= 1 && kv_heads >= 1,
+              "batch, heads and kv_heads must be positive");
+  ENQ_REQUIRE(heads % kv_heads == 0, "heads (%d) must be a multiple of kv_heads (%d)", heads,
+              kv_heads);
+  ENQ_REQUIRE(q && k && v && out, "NULL pointer argument");
+  ENQ_REQUIRE(batch <= 65535 && heads <= 65535, "problem too large");
+  ENQ_REQUIRE(ldq >= int64_t(heads) * head_dim && ldo >= int64_t(heads) * head_dim &&
+                  ldk >= int64_t(kv_heads) * head_dim && ldv >= int64_t(kv_heads) * head_dim,
+              "row strides smaller than the heads they hold");
+  ENQ_REQUIRE(ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && ldo % 4 == 0 && aligned(q, 16) &&
+                  aligned(k, 16) && aligned(v, 16) && aligned(out, 16),
+              "attention needs 16-byte aligned rows");
+}
+
+}  // namespace
+
 extern "C" int enq_attention(const float* q, int64_t ldq, const float* k, int64_t ldk,
                              const float* v, int64_t ldv, int64_t batch, int64_t seq, int heads,
                              int kv_heads, int head_dim, int causal, int64_t window, float* out,
                              int64_t ldo) {
   return guarded([&] {
     require_init();
-    ENQ_REQUIRE(batch >= 1 && seq >= 1 && heads >= 1 && kv_heads >= 1,
-                "batch, seq, heads and kv_heads must be positive");
-    ENQ_REQUIRE(heads % kv_heads == 0, "heads (%d) must be a multiple of kv_heads (%d)", heads,
-                kv_heads);
-    ENQ_REQUIRE(q && k && v && out, "NULL pointer argument");
-    ENQ_REQUIRE(batch <= 65535 && heads <= 65535 && ceil_div(seq, kAttnQ) <= 0x7fffffff,
-                "problem too large");
-    ENQ_REQUIRE(ldq >= int64_t(heads) * head_dim && ldo >= int64_t(heads) * head_dim &&
-                    ldk >= int64_t(kv_heads) * head_dim && ldv >= int64_t(kv_heads) * head_dim,
-                "row strides smaller than the heads they hold");
-    ENQ_REQUIRE(ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && ldo % 4 == 0 &&
-                    aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 16),
-                "attention needs 16-byte aligned rows");
-    AttnShape sh{batch, seq, heads, kv_heads, ldq, ldk, ldv, ldo,
+    ENQ_REQUIRE(seq >= 1, "seq must be positive");
+    check_attention(q, ldq, k, ldk, v, ldv, batch, heads, kv_heads, head_dim, out, ldo);
+    ENQ_REQUIRE(ceil_div(seq, kAttnQ) <= 0x7fffffff, "problem too large");
+    AttnShape sh{batch, seq, seq, heads, kv_heads, ldq, ldk, ldv, ldo, seq, seq, 0, 0,
                  float(1.0 / std::sqrt(double(head_dim))), causal ? 1 : 0, window};
     attention(q, k, v, sh, head_dim, out);
+  });
+}
+
+extern "C" int enq_attention_kv(const float* q, int64_t ldq, int64_t q_bstride, int64_t seq_q,
+                                int64_t q_pos0, const float* k, int64_t ldk, const float* v,
+                                int64_t ldv, int64_t kv_bstride, int64_t seq_k, int64_t k_pos0,
+                                int64_t batch, int heads, int kv_heads, int head_dim, int causal,
+                                int64_t window, float* out, int64_t ldo) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(seq_q >= 1 && seq_k >= 1, "seq_q and seq_k must be positive");
+    ENQ_REQUIRE(q_bstride >= seq_q && kv_bstride >= seq_k, "batch strides below the lengths");
+    check_attention(q, ldq, k, ldk, v, ldv, batch, heads, kv_heads, head_dim, out, ldo);
+    ENQ_REQUIRE(ceil_div(seq_q, kAttnQ) <= 0x7fffffff, "problem too large");
+    AttnShape sh{batch, seq_q, seq_k, heads, kv_heads, ldq, ldk, ldv, ldo, q_bstride, kv_bstride,
+                 q_pos0, k_pos0, float(1.0 / std::sqrt(double(head_dim))), causal ? 1 : 0,
+                 window};
+    attention(q, k, v, sh, head_dim, out);
+  });
+}
+
+extern "C" int enq_add_bcast(const float* a, const float* b, int64_t outer, int64_t inner,
+                             float* y) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(outer >= 0 && inner >= 1, "bad shape");
+    if (outer == 0) return;
+    ENQ_REQUIRE(a && b && y, "NULL pointer argument");
+    add_bcast_kernel<<<stride_grid(outer * inner), 256, 0, stream()>>>(a, b, outer, inner, y);
+    check_launch("add_bcast_kernel");
+  });
+}
+
+extern "C" int enq_copy_rows(const float* src, int64_t ld_src, int64_t src_bstride,
+                             const int32_t* rows, float* dst, int64_t ld_dst,
+                             int64_t dst_bstride, int64_t nrows, int64_t width, int64_t batch) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(nrows >= 0 && width >= 0 && batch >= 0, "bad shape");
+    if (nrows == 0 || width == 0 || batch == 0) return;
+    ENQ_REQUIRE(src && dst, "NULL pointer argument");
+    ENQ_REQUIRE(ld_src >= width && ld_dst >= width, "row pitch below the width");
+    copy_rows_kernel<<<stride_grid(batch * nrows * width), 256, 0, stream()>>>(
+        src, ld_src, src_bstride, rows, dst, ld_dst, dst_bstride, nrows, width, batch);
+    check_launch("copy_rows_kernel");
   });
 }

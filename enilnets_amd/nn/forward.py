@@ -17,7 +17,8 @@ import numpy as np
 from ..device import DeviceArray
 from .dense import act_quant, act_quant_args, dense_w8
 from .moe import moe_forward
-from .transformer import layernorm, mha_forward, residual_add
+from .transformer import (embedding, layernorm, mha_forward, positional_encoding,
+                          residual_add)
 from .weights import int8_weights
 
 #: Activations whose NumPy result is float64 for a float32 input, because
@@ -53,7 +54,8 @@ def Forward(model: Any, inputs: Any, training: bool = False, dropout_rate: float
     ("fp32": fp32-accurate, "bf16": bf16 activations).
 
     Layer types: dense/sparse, layernorm, multihead_attention (softmax),
-    residual_save, residual_add and moe.  Every layer computes in float32 on
+    residual_save, residual_add, moe, embedding, positional_encoding and
+    dropout (inference).  Every layer computes in float32 on
     the device; the host copy of each output takes the dtype NumPy gives the
     reference's expression (float64 after GELU, ``forward.py:32``; after
     attention, whose scores are divided by the float64 ``np.sqrt(Dh)``,
@@ -80,6 +82,20 @@ def Forward(model: Any, inputs: Any, training: bool = False, dropout_rate: float
             y = mha_forward(cur, layer, variant, training)
             dtype = np.float64
         elif kind == "residual_save":
+            y, dtype = cur, cur_dtype
+        elif kind == "embedding":
+            # indices come from the host input, as forward.py:414-422 reads them
+            y = embedding(outputs[-1], layer)
+            dtype = np.asarray(layer["weights"]).dtype
+        elif kind == "positional_encoding":
+            y = positional_encoding(cur, layer)
+            key = "weights" if layer.get("_pos_type") == "learnable" else "pe"
+            dtype = np.result_type(cur_dtype, np.asarray(layer[key]).dtype)
+        elif kind == "dropout":
+            rate = layer.get("rate", dropout_rate)
+            if training and rate > 0:
+                raise NotImplementedError("training-mode dropout is not on the quantized path")
+            layer["mask"] = None
             y, dtype = cur, cur_dtype
         elif kind == "residual_add":
             idx = layer["save_index"]

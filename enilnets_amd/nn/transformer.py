@@ -67,6 +67,53 @@ def residual_add(x: DeviceArray, saved: DeviceArray,
     return y
 
 
+def token_rows(tokens: Any, vocab: int) -> np.ndarray:
+    """Token ids as the embedding rows NumPy indexing would read
+    (``forward.py:414-422``): int32 ids, negative ids counted from the end,
+    IndexError outside ``[-vocab, vocab)``; a 1-D input is one token per row."""
+    ids = np.asarray(tokens, dtype=np.int32)
+    if ids.ndim == 1:
+        ids = ids.reshape(-1, 1)
+    bad = (ids < -vocab) | (ids >= vocab)
+    if bad.any():
+        raise IndexError(f"index {int(ids[bad].reshape(-1)[0])} is out of bounds for axis 0 "
+                         f"with size {vocab}")
+    return np.ascontiguousarray(np.where(ids < 0, ids + vocab, ids), dtype=np.int32)
+
+
+def embedding(tokens: Any, layer: Dict[str, Any]) -> DeviceArray:
+    """``layer["weights"][ids]`` gathered on the device."""
+    from .weights import device_table
+    table = device_table(layer, "weights")
+    vocab, width = table.shape
+    ids = token_rows(tokens, vocab)
+    d_ids = DeviceArray.from_numpy(ids)
+    out = DeviceArray(ids.shape + (width,), np.float32)
+    _lib.call("enq_copy_rows", table.ptr, width, 0, d_ids.ptr, out.ptr, width, 0, ids.size,
+              width, 1)
+    return out
+
+
+def positional_encoding(x: DeviceArray, layer: Dict[str, Any], pos: int = 0,
+                        out: Optional[DeviceArray] = None) -> DeviceArray:
+    """``x + table[pos:pos+S][None]`` (``forward.py:597-603``; a KV-cache
+    step passes its first absolute position, ``kvcache.py:88-91``)."""
+    from .weights import device_table
+    if len(x.shape) != 3:
+        raise ValueError(f"positional encoding expects (batch, seq, embed), got {x.shape}")
+    key = "weights" if layer.get("_pos_type") == "learnable" else "pe"
+    table = device_table(layer, key)
+    B, S, E = x.shape
+    if table.shape[1] != E:
+        raise ValueError(f"table width {table.shape[1]} does not match {E}")
+    if pos + S > table.shape[0]:
+        raise ValueError(f"operands could not be broadcast together: positions {pos}..{pos + S} "
+                         f"of a {table.shape[0]}-row table")
+    y = out if out is not None else DeviceArray(x.shape, np.float32)
+    _lib.call("enq_add_bcast", x.ptr, _at(table, 4 * pos * E), B, S * E, y.ptr)
+    return y
+
+
 def _fused_qkv(layer: Dict[str, Any]) -> Tuple[Int8Weights, int, int]:
     """int8 codes and row scales of ``[Wq; Wk; Wv]`` in one device buffer,
     rebuilt whenever one of the three cached weights is."""

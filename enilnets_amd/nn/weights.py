@@ -137,3 +137,42 @@ def int8_weights(layer: Dict[str, Any], name: str) -> Int8Weights:
     entry = Int8Weights.from_fake(source, spec)
     store_int8(layer, name, entry)
     return entry
+
+
+_TABLE_KEY = "_state_enq_tables"
+
+
+class DeviceTable:
+    """A float32 device copy of a layer's float table (embedding and
+    positional tables), checked against its host array like the int8 cache."""
+
+    __slots__ = ("data", "source_id", "source_digest")
+
+    def __init__(self, host: np.ndarray):
+        self.data = DeviceArray.from_numpy(np.ascontiguousarray(host, dtype=np.float32))
+        self.source_id = id(host)
+        self.source_digest = _digest(host)
+
+    def __deepcopy__(self, memo):
+        return None
+
+    def matches(self, host: np.ndarray) -> bool:
+        return self.source_id == id(host) and self.source_digest == _digest(host)
+
+
+def device_table(layer: Dict[str, Any], name: str) -> DeviceArray:
+    """``layer[name]`` as a float32 device array, uploaded again only when
+    the host array was replaced or changed."""
+    host = np.asarray(layer[name])
+    if host.dtype != np.float32:
+        raise NotImplementedError(f"{name} of dtype {host.dtype}: the device path takes "
+                                  "float32 tables")
+    cache = layer.get(_TABLE_KEY)
+    if cache is None:
+        cache = {}
+        layer[_TABLE_KEY] = cache
+    entry = cache.get(name)
+    if entry is None or not entry.matches(layer[name]):
+        entry = DeviceTable(layer[name])
+        cache[name] = entry
+    return entry.data

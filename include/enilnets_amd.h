@@ -270,6 +270,30 @@ int enq_attention(const float* q, int64_t ldq, const float* k, int64_t ldk,
                   int heads, int kv_heads, int head_dim, int causal,
                   int64_t window, float* out, int64_t ldo);
 
+/* Attention of seq_q new queries over seq_k keys and values (a KV-cache
+ * decode step, Enilnets/nn/kvcache.py:124-213): queries of batch b are rows
+ * b*q_bstride + [0, seq_q) of q and out, keys/values rows b*kv_bstride +
+ * [0, seq_k) of k and v; query i is at absolute position q_pos0 + i, key j
+ * at k_pos0 + j, and the masks of _window_mask apply to those positions.
+ * Otherwise as enq_attention. */
+int enq_attention_kv(const float* q, int64_t ldq, int64_t q_bstride, int64_t seq_q,
+                     int64_t q_pos0, const float* k, int64_t ldk, const float* v,
+                     int64_t ldv, int64_t kv_bstride, int64_t seq_k, int64_t k_pos0,
+                     int64_t batch, int heads, int kv_heads, int head_dim, int causal,
+                     int64_t window, float* out, int64_t ldo);
+
+/* y[o, i] = a[o, i] + b[i] for o < outer, i < inner: the positional-table
+ * add x + table[pos:pos+S][None] of forward.py:597-603 / kvcache.py:88-91. */
+int enq_add_bcast(const float* a, const float* b, int64_t outer, int64_t inner, float* y);
+
+/* Strided row copy over `batch` row blocks: dst[(b*dst_bstride + r)*ld_dst + c]
+ * = src[(b*src_bstride + s)*ld_src + c] for r < nrows, c < width, with s = r,
+ * or s = rows[b*nrows + r] when rows is not NULL (an embedding lookup,
+ * forward.py:414-422, with batch 1).  Appends keys and values to a cache. */
+int enq_copy_rows(const float* src, int64_t ld_src, int64_t src_bstride,
+                  const int32_t* rows, float* dst, int64_t ld_dst, int64_t dst_bstride,
+                  int64_t nrows, int64_t width, int64_t batch);
+
 /* ---- Mixture of experts on int8 expert weights ------------------------
  * Replaces moe_forward, Enilnets/nn/moe.py:52-87, for x (tokens, d) fp32:
  * router logits = x . (wr * sr)^T + br (experts, d) unless router_logits

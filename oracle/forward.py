@@ -212,7 +212,9 @@ def forward(layers: List[Dict[str, Any]], inputs: Any,
     the input), as ``nn/forward.py:272-311,810-811`` does.  Covers the
     layer types of the benchmark configurations: dense, layernorm,
     multihead_attention (softmax, absolute positions), residual_save,
-    residual_add, moe; ``act_quant`` as ``forward.py:798-805``."""
+    residual_add, moe, and the decoding front end: embedding
+    (``:414-422``), positional_encoding (``:597-603``), dropout at inference
+    (``:398-413``); ``act_quant`` as ``forward.py:798-805``."""
     from .quantization import fake_quantize
     x = np.asarray(inputs, dtype=dtype)
     if x.ndim == 1:
@@ -228,6 +230,16 @@ def forward(layers: List[Dict[str, Any]], inputs: Any,
         elif kind == "multihead_attention":
             x = mha_forward(x, layer)
         elif kind == "residual_save":
+            pass
+        elif kind == "embedding":
+            ids = np.asarray(x, dtype=np.int32)
+            if ids.ndim == 1:
+                ids = ids.reshape(-1, 1)
+            x = layer["weights"][ids]
+        elif kind == "positional_encoding":
+            table = layer["weights"] if layer.get("_pos_type") == "learnable" else layer["pe"]
+            x = x + table[:x.shape[1]][None, :, :]
+        elif kind == "dropout":
             pass
         elif kind == "residual_add":
             x = x + outputs[layer["save_index"]]

@@ -445,3 +445,21 @@ def test_layernorm_closed_form():
     assert np.allclose(y.var(axis=-1), var / (var + 1e-5), atol=1e-12)
     L2 = {"gamma": np.arange(16.0), "beta": np.full(16, 0.5)}
     assert np.allclose(oracle.layernorm_forward(np.full((2, 16), 7.0), L2), 0.5)
+
+
+def test_forward_front_end_closed_forms():
+    # forward.py:414-422 (embedding: the table rows of the int ids),
+    # :597-603 (positional table rows added per
+    # position), :398-413 (dropout is the identity at inference)
+    table = np.arange(20, dtype=np.float32).reshape(5, 4)
+    pe = np.full((8, 4), 0.5, np.float32)
+    layers = [{"type": "embedding", "weights": table},
+              {"type": "positional_encoding", "pe": pe, "_pos_type": "sinusoidal"},
+              {"type": "dropout", "rate": 0.5}]
+    out = oracle.forward(layers, np.array([[4, 0, 2]]))
+    assert np.array_equal(out[1], table[[[4, 0, 2]]])
+    assert np.array_equal(out[2], table[[[4, 0, 2]]] + 0.5)
+    assert out[3] is out[2]
+    # Forward makes a 1-D input one row first (forward.py:286-287)
+    one = oracle.forward(layers[:1], np.array([3, 1]))
+    assert one[1].shape == (1, 2, 4) and np.array_equal(one[1][0], table[[3, 1]])
