@@ -17,6 +17,7 @@ from .quantization import (QUANTIZABLE, compute_scale, dequantize,
                            fake_quantize, quant_range, quantization_error,
                            quantize, quantize_tensor, quantize_weights,
                            int8_codes)
+from .qat import MovingRange, qat_linear_forward, qat_quantized_weight, ste_mask
 from .forward import (activate, dense_forward, forward, forward_top_k, layernorm_forward,
                       mha_forward, moe_forward, router, top_k, w8a8_dense, window_mask)
 
@@ -25,5 +26,6 @@ __all__ = [
     "quant_range", "quantization_error", "quantize", "quantize_tensor",
     "quantize_weights", "int8_codes", "activate", "dense_forward", "forward",
     "layernorm_forward", "mha_forward", "moe_forward", "w8a8_dense", "forward_top_k",
-    "router", "top_k", "window_mask",
+    "router", "top_k", "window_mask", "MovingRange", "qat_linear_forward",
+    "qat_quantized_weight", "ste_mask",
 ]

@@ -463,3 +463,33 @@ def test_forward_front_end_closed_forms():
     # Forward makes a 1-D input one row first (forward.py:286-287)
     one = oracle.forward(layers[:1], np.array([3, 1]))
     assert one[1].shape == (1, 2, 4) and np.array_equal(one[1][0], table[[3, 1]])
+
+
+def test_qat_weight_is_per_channel_quantize_tensor():
+    # graph/quantization.py:119-130 takes min / max over every axis but 0 and
+    # fake-quantizes symmetrically: exactly quantize_tensor(per_channel=True)
+    rng = np.random.default_rng(41)
+    w = (rng.standard_normal((12, 30)) * 0.2).astype(np.float32)
+    fq = oracle.qat_quantized_weight(w, 8, per_channel=True)
+    want, _, _ = oracle.quantize_tensor(w, 8, "symmetric", per_channel=True)
+    assert fq.dtype == want.dtype and np.array_equal(fq, want)
+    fq1 = oracle.qat_quantized_weight(w, 4, per_channel=False)
+    want1, _, _ = oracle.quantize_tensor(w, 4, "symmetric", per_channel=False)
+    assert np.array_equal(fq1, want1)
+    # a planted mistake: statistics over axis 0 instead of axis 1
+    wrong = oracle.fake_quantize(w, *oracle.compute_scale(w.min(0, keepdims=True),
+                                                          w.max(0, keepdims=True), 8,
+                                                          "symmetric"), 8, "symmetric")
+    assert not np.array_equal(fq, wrong)
+
+
+def test_qat_observer_and_ste_mask_closed_forms():
+    obs = oracle.MovingRange(momentum=0.5)
+    obs.observe(np.array([-1.0, 3.0]))
+    obs.observe(np.array([-3.0, 1.0]))
+    assert (obs.low, obs.high) == (-2.0, 2.0)
+    s, z = obs.scale_and_zero_point(8, "asymmetric")
+    assert np.isclose(s, 4.0 / 255) and z == np.round(0 - (-2.0) / s)
+    x = np.array([-1.0, -0.5, 0.0, 0.5, 1.0])
+    m = oracle.ste_mask(x, 0.5 / 127, 0.0, 8, "symmetric")
+    assert m.tolist() == [False, True, True, True, False]
