@@ -448,14 +448,16 @@ def main():
                                "per-output-channel int8 weights",
                    "global_batch": 4096, "layers": 3, "variant": "fp32",
                    "flops_per_step": flops},
-        "roofline": {"bound": "mfma", "kernel": "w8_ring_kernel (+ split_planes_kernel)",
+        "roofline": {"bound": "mfma", "kernel": "w8_ring_kernel<RingCfg<128,128,4,2,2,4,fused A>>",
                      "shape": [dom["m"], dom["n"], dom["k"]],
                      "achieved": round(dom_tf, 3), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(dom_tf / BF16_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic("mlp_layer_gemm", [dom["m"], dom["n"], dom["k"]]),
                      "note": "algorithmic 2*M*N*K over the measured time of the layer's "
-                             "dense call; the fp32-accurate path issues two bf16 MFMA "
-                             "passes (hi, lo) per product"},
+                             "dense call, one kernel that splits the fp32 activations "
+                             "itself; the fp32-accurate path issues two bf16 MFMA "
+                             "passes (hi, lo) per product, so its ceiling is half the "
+                             "bf16 peak"},
     }
     if not args.no_components:
         result["components"] = components(timer, rng, args.only)

@@ -61,10 +61,10 @@ void act_quant(const float* x, int64_t n, const Epilogue& ep, float* y) {
   check_launch("act_quant_kernel");
 }
 
-void finish_rows(float* y, int64_t m, int64_t n, const Epilogue& ep) {
-  if (ep.activation != ENQ_ACT_SOFTMAX) return;
-  softmax_rows(y, m, n);
-  act_quant(y, m * n, ep, y);
+void finish_rows(float* y, int64_t m, int64_t n, const Epilogue& ep, bool fused_aq) {
+  const bool softmax = ep.activation == ENQ_ACT_SOFTMAX;
+  if (softmax) softmax_rows(y, m, n);
+  if (softmax || !fused_aq) act_quant(y, m * n, ep, y);
 }
 
 bool valid_act_quant(int mode, double scale, float qmin, float qmax) {

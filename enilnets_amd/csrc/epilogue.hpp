@@ -83,11 +83,17 @@ __device__ __forceinline__ float epilogue_out(float x, const Epilogue& e) {
   return e.aq != ENQ_AQ_NONE ? fake_quant(a, e) : a;
 }
 
-template <class Body>
+// FUSE_AQ instantiates the fake-quantizing variant too.  Kernels without
+// register headroom (the 256 x 256 tiles) leave it out: its float64
+// arithmetic next to live accumulators spills them, so their callers run the
+// fake-quantization as a separate pass (gemm_epilogue / finish_rows).
+template <bool FUSE_AQ, class Body>
 __device__ __forceinline__ void with_activation(const Epilogue& ep, Body&& body) {
-  if (ep.aq != ENQ_AQ_NONE) {
-    body([ep](float x) { return epilogue_out(x, ep); });
-    return;
+  if constexpr (FUSE_AQ) {
+    if (ep.aq != ENQ_AQ_NONE) {
+      body([ep](float x) { return epilogue_out(x, ep); });
+      return;
+    }
   }
   switch (ep.activation) {
     case ENQ_ACT_LINEAR:
@@ -107,16 +113,17 @@ __device__ __forceinline__ void with_activation(const Epilogue& ep, Body&& body)
 void softmax_rows(float* y, int64_t m, int64_t n);
 
 // The epilogue a GEMM applies itself: a softmax activation runs afterwards
-// as a row kernel, so its fake-quantization must wait for it.
-inline Epilogue gemm_epilogue(const Epilogue& ep) {
+// as a row kernel, so its fake-quantization must wait for it; a kernel that
+// does not fuse the fake-quantization leaves it to finish_rows as well.
+inline Epilogue gemm_epilogue(const Epilogue& ep, bool fuse_aq) {
   Epilogue e = ep;
-  if (e.activation == ENQ_ACT_SOFTMAX) e.aq = ENQ_AQ_NONE;
+  if (e.activation == ENQ_ACT_SOFTMAX || !fuse_aq) e.aq = ENQ_AQ_NONE;
   return e;
 }
 
-// Row softmax (if the activation is softmax) and the deferred
-// fake-quantization, after a GEMM that applied gemm_epilogue(ep).
-void finish_rows(float* y, int64_t m, int64_t n, const Epilogue& ep);
+// Row softmax (if the activation is softmax) and the fake-quantization the
+// GEMM did not apply, after a GEMM that ran gemm_epilogue(ep, fused_aq).
+void finish_rows(float* y, int64_t m, int64_t n, const Epilogue& ep, bool fused_aq);
 
 // y = fake_quant(x) over n values (in place allowed).
 void act_quant(const float* x, int64_t n, const Epilogue& ep, float* y);

@@ -452,7 +452,7 @@ __global__ __launch_bounds__(WM * WN * 64) void w8_gemm_kernel(
           float v = acc[i][j][e] * s;
           if (bias) v = v + b;
           if (z) z[row * n + col] = v;
-          y[row * n + col] = epilogue_out(v, ep);
+          y[row * n + col] = activate(v, ep);
         }
       }
   }
@@ -472,33 +472,44 @@ __global__ __launch_bounds__(WM * WN * 64) void w8_gemm_kernel(
 // 32x32x16 MFMA steps take k 16 g + [0, 8) and 16 g + [8, 16), i.e. chunks
 // 2 g and 2 g + 1 of an A or bf16 B row.
 // ---------------------------------------------------------------------------
-template <int BM_, int BN_, int WM_, int WN_, int PLANES_, int STAGES_>
+// FUSED_A: A arrives as the fp32 activations themselves (128-byte rows per
+// stage, 16-byte chunks swapped on bit 1 of the row: swz128) and each stage
+// is split into bf16 hi / lo planes once per workgroup, into a
+// double-buffered copy laid out like the split planes; no separate pass.
+template <int BM_, int BN_, int WM_, int WN_, int PLANES_, int STAGES_, bool FUSED_A_ = false>
 struct RingCfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, PLANES = PLANES_;
   static constexpr int STAGES = STAGES_, BK = 32;
+  static constexpr bool FUSED_A = FUSED_A_;
   static constexpr int NT = WM * WN * 64;
   static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-  static constexpr int A_BYTES = PLANES * BM * 64;   // bf16 rows of 64 bytes
+  // bf16 plane rows of 64 bytes, or fp32 rows of 128 bytes
+  static constexpr int A_BYTES = FUSED_A ? BM * 128 : PLANES * BM * 64;
   static constexpr int B_BYTES = BN * 32;            // code rows of 32 bytes
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int BCONV_BYTES = BN * 64;         // one bf16 copy of a B tile
+  static constexpr int ACONV_BYTES = FUSED_A ? PLANES * BM * 64 : 0;  // one split copy of A
   static constexpr int A_BLOCKS = A_BYTES / 1024, B_BLOCKS = B_BYTES / 1024;
   static constexpr int BLOCKS = A_BLOCKS + B_BLOCKS;
   // every wave issues the same number of 1 KiB blocks (vmcnt accounting);
   // waves past the last block repeat it, rewriting identical bytes
   static constexpr int DMA_PER_WAVE = (BLOCKS + NT / 64 - 1) / (NT / 64);
   static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole 1 KiB blocks");
-  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES + 2 * BCONV_BYTES;
+  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES + 2 * BCONV_BYTES + 2 * ACONV_BYTES;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
   static_assert(NT >= 2 * BN, "one expansion item per thread");
+  static_assert(!FUSED_A || NT >= 4 * BM, "one split item per thread");
 };
 
 __device__ __forceinline__ int swz32(int row, int half) { return half ^ ((row >> 3) & 1); }
+// fp32 A rows: 16-byte chunks XOR bit 1 of the row, so the 16 lanes reading
+// chunk 2c (or 2c + 1) of four consecutive rows hit distinct banks.
+__device__ __forceinline__ int swz128(int row, int chunk) { return chunk ^ ((row >> 1) & 1); }
 
 template <class C, bool KTAIL>
 __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
     const uint16_t* __restrict__ xa, int64_t plane_stride, int64_t kp,
-    const int8_t* __restrict__ w, const float* __restrict__ scale,
+    const float* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ scale,
     const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n,
     RowGroups grp, Epilogue ep, float* __restrict__ y, float* __restrict__ z) {
   constexpr int BM = C::BM, BN = C::BN, WN = C::WN, PLANES = C::PLANES, STAGES = C::STAGES;
@@ -523,14 +534,23 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
   }
 
   // DMA sources.  Block b (of A_BLOCKS + B_BLOCKS per stage) is handled by
-  // wave b / DPW.  A block: 16 rows x 64 B of one plane; B block: 32 rows x 32 B.
+  // wave b / DPW.  A block: 16 rows x 64 B of one plane (fused: 8 rows x
+  // 128 B of fp32); B block: 32 rows x 32 B.
   const char* src[DPW];
   int src_koff[DPW];   // byte offset of this lane's chunk inside a stage's K range
   bool is_b[DPW];
 #pragma unroll
   for (int j = 0; j < DPW; ++j) {
     const int blk = min(wave * DPW + j, C::BLOCKS - 1);
-    if (blk < C::A_BLOCKS) {
+    if (C::FUSED_A && blk < C::A_BLOCKS) {
+      const int r = blk * 8 + (lane >> 3);
+      const int chunk = swz128(r, lane & 7);                // logical chunk: 4 floats
+      int64_t g = m0 + r;
+      g = g < m ? g : m - 1;
+      src[j] = reinterpret_cast<const char*>(x + g * k);
+      src_koff[j] = chunk * 16;
+      is_b[j] = false;
+    } else if (blk < C::A_BLOCKS) {
       const int r_all = blk * 16 + (lane >> 2);          // row within the PLANES x BM rows
       const int p = r_all / BM, r = r_all % BM;
       const int chunk = swz64(r, lane & 3);                 // logical 16-byte chunk
@@ -561,6 +581,11 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
       if (is_b[j]) {
         const int64_t kb = int64_t(t) * BK + src_koff[j];
         sp = (KTAIL && kb >= k) ? zero : static_cast<const void*>(src[j] + kb);
+      } else if (C::FUSED_A) {
+        const int64_t ke = int64_t(t) * BK + src_koff[j] / 4;  // first column of the chunk
+        sp = (KTAIL && ke >= k) ? zero
+                                : static_cast<const void*>(src[j] + int64_t(t) * BK * 4 +
+                                                           src_koff[j]);
       } else {
         sp = src[j] + int64_t(t) * BK * 2 + src_koff[j];
       }
@@ -588,8 +613,10 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
   const int lrow = lane & 31, g = lane >> 5;
 
   // bf16 copies of the B tiles, double-buffered after the ring: each tile
-  // is expanded once per workgroup instead of once per wave that reads it
+  // is expanded once per workgroup instead of once per wave that reads it;
+  // likewise the split A planes of the fused variant
   char* bconv = lds + STAGES * C::STAGE_BYTES;
+  char* aconv = bconv + 2 * C::BCONV_BYTES;
   int a_off[PLANES][FM][2], b_off[FN][2];
 #pragma unroll
   for (int p = 0; p < PLANES; ++p)
@@ -613,19 +640,40 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
   const int conv_src = C::A_BYTES + cr * 32 + 16 * swz32(cr, ch);
   const int conv_dst0 = cr * 64 + 16 * swz64(cr, 2 * ch);
   const int conv_dst1 = cr * 64 + 16 * swz64(cr, 2 * ch + 1);
+  // fused split item of this thread: 8 floats (logical chunks 2 ag and
+  // 2 ag + 1) of A row ar, which become chunk ag of that row in each plane
+  const bool splits = C::FUSED_A && tid < 4 * BM;
+  const int ar = tid >> 2, ag = tid & 3;
+  const int split_src0 = ar * 128 + 16 * swz128(ar, 2 * ag);
+  const int split_src1 = ar * 128 + 16 * swz128(ar, 2 * ag + 1);
+  const int split_dst = ar * 64 + 16 * swz64(ar, ag);
   auto convert = [&](int t) {
-    if (!converts) return;
-    const int4 raw =
-        *reinterpret_cast<const int4*>(lds + (t % STAGES) * C::STAGE_BYTES + conv_src);
-    bf16x8 first, second;
-    codes16_to_bf16(raw, first, second);
-    char* dst = bconv + (t & 1) * C::BCONV_BYTES;
-    *reinterpret_cast<bf16x8*>(dst + conv_dst0) = first;
-    *reinterpret_cast<bf16x8*>(dst + conv_dst1) = second;
+    const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
+    if (converts) {
+      const int4 raw = *reinterpret_cast<const int4*>(st + conv_src);
+      bf16x8 first, second;
+      codes16_to_bf16(raw, first, second);
+      char* dst = bconv + (t & 1) * C::BCONV_BYTES;
+      *reinterpret_cast<bf16x8*>(dst + conv_dst0) = first;
+      *reinterpret_cast<bf16x8*>(dst + conv_dst1) = second;
+    }
+    if constexpr (C::FUSED_A) {
+      if (splits) {
+        const float4 a = *reinterpret_cast<const float4*>(st + split_src0);
+        const float4 b = *reinterpret_cast<const float4*>(st + split_src1);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        Pack8 hi, lo;
+        split8<PLANES>(v, hi, lo);
+        char* dst = aconv + (t & 1) * C::ACONV_BYTES;
+        *reinterpret_cast<Pack8*>(dst + split_dst) = hi;
+        if (PLANES == 2) *reinterpret_cast<Pack8*>(dst + BM * 64 + split_dst) = lo;
+      }
+    }
   };
   bf16x8 fa[PLANES][FM][2], fb[FN][2];
   auto read_frags = [&](int t) {
-    const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
+    const char* st = C::FUSED_A ? aconv + (t & 1) * C::ACONV_BYTES
+                                : lds + (t % STAGES) * C::STAGE_BYTES;
     const char* bt = bconv + (t & 1) * C::BCONV_BYTES;
 #pragma unroll
     for (int j = 0; j < FN; ++j)
@@ -672,7 +720,7 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
   }
 
   const int lhalf = lane >> 5;
-  with_activation(ep, [&](auto act) {
+  with_activation<(C::BM <= 128)>(ep, [&](auto act) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int64_t col = n0 + wn * TN + j * 32 + lrow;
@@ -698,7 +746,8 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
 template <class C>
 void launch_w8_ring(const uint16_t* xa, int64_t plane_stride, int64_t kp, const int8_t* w,
                     const float* scale, const float* bias, int64_t m, int64_t n, int64_t k,
-                    const Epilogue& ep, float* y, float* z, const RowGroups& grp) {
+                    const Epilogue& ep, float* y, float* z, const RowGroups& grp,
+                    const float* x = nullptr) {
   // grouped rows: every group may end in a partial tile
   const int64_t tiles_m = ceil_div(m, C::BM) + (grp.offsets ? grp.groups : 0);
   const int64_t tiles_n = ceil_div(n, C::BN);
@@ -714,7 +763,7 @@ void launch_w8_ring(const uint16_t* xa, int64_t plane_stride, int64_t kp, const 
   }
   auto kernel = (k % C::BK == 0) ? w8_ring_kernel<C, false> : w8_ring_kernel<C, true>;
   kernel<<<unsigned(tiles_m * tiles_n), C::NT, lds_bytes, stream()>>>(
-      xa, plane_stride, kp, w, scale, bias, m, n, k, int(tiles_m), int(tiles_n), grp, ep, y, z);
+      xa, plane_stride, kp, x, w, scale, bias, m, n, k, int(tiles_m), int(tiles_n), grp, ep, y, z);
   check_launch("w8_ring_kernel");
 }
 
@@ -904,7 +953,6 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
               int64_t n, const float* bias, const Epilogue& ep_all, int variant, float* y,
               float* z) {
   const int planes = variant == ENQ_W8_FP32 ? 2 : 1;
-  const Epilogue ep = gemm_epilogue(ep_all);
   // split-K GEMV for few activation rows, and for tall-skinny outputs (one
   // 16-row block per grid z index, so at most 65535 * 16 rows); both read
   // the fp32 activations directly
@@ -926,6 +974,12 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
       else run(P1{}, K2{});
     }
   };
+  // the GEMV finish kernel and the 128 x 128 kernel fuse the activation
+  // fake-quantization; the other GEMM kernels leave it to finish_rows
+  const bool big = ceil_div(m, 256) * ceil_div(n, 256) >= device_cu_count();
+  const bool fused_mid = !gemv && !big && kmode != 2 && k % 4 == 0 && aligned(x, 16);
+  const bool fuse_aq = gemv || fused_mid;
+  const Epilogue ep = gemm_epilogue(ep_all, fuse_aq);
   if (gemv) {
     const GemvPlan plan = plan_gemv(m, n, k);
     auto* part = static_cast<float*>(workspace(plan.part_bytes(n)));
@@ -937,15 +991,25 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
     });
   } else {
     const int64_t kp = ceil_div(k, kBK) * kBK;
-    const int64_t plane_stride = m * kp;
-    auto* xa = static_cast<uint16_t*>(workspace(size_t(planes) * plane_stride * sizeof(uint16_t)));
-    split_planes(x, nullptr, m, k, xa, m, kp, planes);
-    with_modes(kmode, [&](auto planes_tag, auto kmode_tag) {
-      gemm_dispatch<decltype(planes_tag)::value, decltype(kmode_tag)::value>(
-          xa, plane_stride, kp, codes, k, w_scale, bias, m, n, k, ep, y, z);
-    });
+    if (fused_mid) {
+      // mid-size GEMM: the 128 x 128 kernel splits the activations itself
+      with_modes(kmode, [&](auto planes_tag, auto) {
+        constexpr int P = decltype(planes_tag)::value;
+        launch_w8_ring<RingCfg<128, 128, 4, 2, P, 4, true>>(nullptr, 0, kp, codes, w_scale, bias,
+                                                            m, n, k, ep, y, z, RowGroups{}, x);
+      });
+    } else {
+      const int64_t plane_stride = m * kp;
+      auto* xa =
+          static_cast<uint16_t*>(workspace(size_t(planes) * plane_stride * sizeof(uint16_t)));
+      split_planes(x, nullptr, m, k, xa, m, kp, planes);
+      with_modes(kmode, [&](auto planes_tag, auto kmode_tag) {
+        gemm_dispatch<decltype(planes_tag)::value, decltype(kmode_tag)::value>(
+            xa, plane_stride, kp, codes, k, w_scale, bias, m, n, k, ep, y, z);
+      });
+    }
   }
-  finish_rows(y, m, n, ep_all);
+  finish_rows(y, m, n, ep_all, fuse_aq);
 }
 
 }  // namespace enq

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(WM * WN * 64) void w8a8_gemm_kernel(
           float v = float(a) * x_scale[row];
           v = v * sw;
           if (bias) v = v + b;
-          y[row * n + col] = epilogue_out(v, ep);
+          y[row * n + col] = activate(v, ep);
         }
       }
   }
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(ring::NT, 1) void w8a8_ring_kernel(
       int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * lhalf + (e % 4);
       xs[i][e] = x_scale[row < m ? row : m - 1];
     }
-  with_activation(ep, [&](auto act) {
+  with_activation<false>(ep, [&](auto act) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int64_t col = n0 + wn * TN + j * 32 + lrow;
@@ -416,7 +416,7 @@ void gemm_w8a8(const int8_t* xq, const float* xs, const int8_t* wq, const float*
     w8a8_dispatch<1>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
   else
     w8a8_dispatch<2>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
-  finish_rows(y, m, n, ep);
+  finish_rows(y, m, n, ep, false);
 }
 
 }  // namespace enq
