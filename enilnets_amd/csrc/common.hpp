@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "enilnets_amd.h"
 
@@ -90,6 +91,17 @@ __device__ __forceinline__ double round_even(double v) { return __builtin_rint(v
 
 template <class T>
 __device__ __forceinline__ bool is_nan(T v) { return v != v; }
+
+// f(integral_constant<int, I>) for I in [B, E), unrolled at compile time:
+// register arrays indexed by I stay in registers where a `#pragma unroll`
+// loop whose body is too large to unroll would leave them in scratch.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 // np.clip(v, lo, hi): NaN passes through, -0.0 is kept.
 template <class T>

@@ -517,7 +517,7 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
   constexpr int DPW = C::DMA_PER_WAVE;
   extern __shared__ __align__(16) uint16_t lds_raw[];
   char* lds = reinterpret_cast<char*>(lds_raw);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   int tm, tn;
   xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
   const int ktiles = int(kp / BK);
   const void* zero = g_zero16;
   auto issue = [&](int t) {
-    char* dst = lds + (t % STAGES) * C::STAGE_BYTES;
+    const uint32_t dst = lds_addr(lds) + (t % STAGES) * C::STAGE_BYTES;
 #pragma unroll
     for (int j = 0; j < DPW; ++j) {
       const int blk = min(wave * DPW + j, C::BLOCKS - 1);

@@ -9,8 +9,6 @@
 //   (acc.astype(float32) * x_scale) * w_scale.T + b.
 #pragma clang fp contract(off)
 
-#include <cstdlib>
-
 #include "common.hpp"
 #include "epilogue.hpp"
 #include "mfma.hpp"
@@ -180,24 +178,31 @@ __global__ __launch_bounds__(WM * WN * 64) void w8a8_gemm_kernel(
 // bank-conflict free.  Requires k % 16 == 0 and 16-byte aligned operands;
 // 16-byte chunks past k are read from a zero block.
 // ---------------------------------------------------------------------------
-namespace ring {
-constexpr int BM = 256, BN = 256, BK = 64, STAGES = 4;
-constexpr int WM = 4, WN = 2, NT = WM * WN * 64;
-constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-constexpr int ROWS = BM + BN;                      // rows per stage (A then B)
-constexpr int STAGE_BYTES = ROWS * BK;             // 32 KiB
-constexpr int DMA_PER_WAVE = ROWS / 16 / (NT / 64);  // 1 KiB blocks per wave per stage
-}  // namespace ring
+template <int WM_, int WN_>
+struct RingShape {
+  static constexpr int BM = 256, BN = 256, BK = 64, STAGES = 4;
+  static constexpr int WM = WM_, WN = WN_, NT = WM * WN * 64;
+  static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  static constexpr int ROWS = BM + BN;                      // rows per stage (A then B)
+  static constexpr int STAGE_BYTES = ROWS * BK;             // 32 KiB
+  static constexpr int DMA_PER_WAVE = ROWS / 16 / (NT / 64);  // 1 KiB blocks per wave per stage
+};
+// 4 x 2 waves of 64 x 128: two waves per SIMD.  2 x 2 waves of 128 x 128 read
+// a third less LDS per MFMA but measured 13% slower at 8192^3: with one wave
+// per SIMD nothing covers the per-stage barrier and wait.
+using W8a8Ring = RingShape<4, 2>;
 
-template <bool KTAIL>
-__global__ __launch_bounds__(ring::NT, 1) void w8a8_ring_kernel(
+template <class R, bool KTAIL>
+__global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ x_scale,
     const int8_t* __restrict__ wq, const float* __restrict__ w_scale,
     const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n,
     Epilogue ep, float* __restrict__ y, int32_t* __restrict__ acc_out) {
-  using namespace ring;
+  constexpr int BM = R::BM, BN = R::BN, BK = R::BK, STAGES = R::STAGES;
+  constexpr int WN = R::WN, TM = R::TM, TN = R::TN, FM = R::FM, FN = R::FN;
+  constexpr int STAGE_BYTES = R::STAGE_BYTES, DMA_PER_WAVE = R::DMA_PER_WAVE;
   extern __shared__ __align__(16) int8_t lds8[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   int tm, tn;
   xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
@@ -224,7 +229,7 @@ __global__ __launch_bounds__(ring::NT, 1) void w8a8_ring_kernel(
   const int ktiles = int(ceil_div(k, BK));
   const void* zero = g_zero16;
   auto issue = [&](int t) {
-    int8_t* dst = lds8 + (t % STAGES) * STAGE_BYTES + wave * DMA_PER_WAVE * 1024;
+    const uint32_t dst = lds_addr(lds8) + (t % STAGES) * STAGE_BYTES + wave * DMA_PER_WAVE * 1024;
     const int64_t k0 = int64_t(t) * BK;
 #pragma unroll
     for (int j = 0; j < DMA_PER_WAVE; ++j) {
@@ -316,57 +321,64 @@ __global__ __launch_bounds__(ring::NT, 1) void w8a8_ring_kernel(
   }
 
   // epilogue: lane holds column l % 32; register e holds row
-  // 8 * (e / 4) + 4 * (l / 32) + e % 4 of each 32 x 32 block
-  float xs[FM][16];
+  // 8 * (e / 4) + 4 * (l / 32) + e % 4 of each 32 x 32 block.  One block row
+  // at a time, so only its 16 row scales are live beside the accumulators.
+  float sw[FN], bj[FN];
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * lhalf + (e % 4);
-      xs[i][e] = x_scale[row < m ? row : m - 1];
-    }
+  for (int j = 0; j < FN; ++j) {
+    int64_t col = n0 + wn * TN + j * 32 + lrow;
+    col = col < n ? col : n - 1;
+    sw[j] = w_scale[col];
+    bj[j] = bias ? bias[col] : 0.f;
+  }
   with_activation<false>(ep, [&](auto act) {
+    static_for<0, FM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      float xs[16];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t col = n0 + wn * TN + j * 32 + lrow;
-      if (col >= n) continue;
-      const float sw = w_scale[col];
-      const float b = bias ? bias[col] : 0.f;
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * lhalf + (e % 4);
+        xs[e] = x_scale[row < m ? row : m - 1];
+      }
+      const int64_t row0 = m0 + wm * TM + i * 32 + 4 * lhalf;
+      static_for<0, FN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t col = n0 + wn * TN + j * 32 + lrow;
+        if (col >= n) return;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * lhalf + (e % 4);
+          const int64_t row = row0 + 8 * (e / 4) + (e % 4);
           if (row < m) {
             const int32_t a = acc[i][j][e];
             if (acc_out) acc_out[row * n + col] = a;
-            float v = float(a) * xs[i][e];
-            v = v * sw;
-            if (bias) v = v + b;
+            float v = float(a) * xs[e];
+            v = v * sw[j];
+            if (bias) v = v + bj[j];
             y[row * n + col] = act(v);
           }
         }
-    }
+      });
+    });
   });
 }
 
+template <class R>
 void launch_w8a8_ring(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws,
                       const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep,
                       float* y, int32_t* acc) {
-  using namespace ring;
-  const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
+  const int64_t tiles_m = ceil_div(m, R::BM), tiles_n = ceil_div(n, R::BN);
   ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
-  const size_t lds_bytes = size_t(STAGES) * STAGE_BYTES;
+  const size_t lds_bytes = size_t(R::STAGES) * R::STAGE_BYTES;
   static bool attr_set = false;
   if (!attr_set) {
-    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8a8_ring_kernel<false>),
+    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8a8_ring_kernel<R, false>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
-    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8a8_ring_kernel<true>),
+    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8a8_ring_kernel<R, true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
     attr_set = true;
   }
-  auto kernel = (k % BK == 0) ? w8a8_ring_kernel<false> : w8a8_ring_kernel<true>;
-  kernel<<<unsigned(tiles_m * tiles_n), NT, lds_bytes, stream()>>>(
+  auto kernel = (k % R::BK == 0) ? w8a8_ring_kernel<R, false> : w8a8_ring_kernel<R, true>;
+  kernel<<<unsigned(tiles_m * tiles_n), R::NT, lds_bytes, stream()>>>(
       xq, xs, wq, ws, bias, m, n, k, int(tiles_m), int(tiles_n), ep, y, acc);
   check_launch("w8a8_ring_kernel");
 }
@@ -408,8 +420,9 @@ void gemm_w8a8(const int8_t* xq, const float* xs, const int8_t* wq, const float*
                int32_t* acc) {
   const bool al = aligned(xq, 16) && aligned(wq, 16);
   const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256);
-  if (k % 16 == 0 && al && big_tiles >= device_cu_count() / 2)
-    launch_w8a8_ring(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+  if (k % 16 == 0 && al && big_tiles >= device_cu_count() / 2) {
+    launch_w8a8_ring<W8a8Ring>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+  }
   else if (k % kBK8 == 0 && al)
     w8a8_dispatch<0>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
   else if (k % 16 == 0 && al)

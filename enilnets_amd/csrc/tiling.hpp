@@ -85,13 +85,31 @@ __device__ __forceinline__ void block_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// 16 bytes from global memory straight into LDS (gfx950 global_load_lds_dwordx4).
-// LDS destination of lane l is lds_base + 16 * l: one instruction fills 1 KiB.
-__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds(
-      (__attribute__((address_space(1))) void*)(const_cast<void*>(src)),
-      (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
+// LDS byte address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
 }
+
+// 16 bytes from global memory straight into LDS (gfx950 global_load_lds_dwordx4).
+// LDS destination of lane l is lds_base + 16 * l: one instruction fills 1 KiB;
+// lds_base must be uniform across the wave (it goes through M0).
+//
+// Written as inline assembly on purpose: the compiler's wait-count pass
+// treats the intrinsic as an LDS access that may complete out of order, and
+// then turns every later partial LDS wait (s_waitcnt lgkmcnt(N)) into a full
+// drain, which serialises each MFMA step behind its own fragment reads.  The
+// instruction only counts on vmcnt; callers order it with explicit vmcnt
+// waits and workgroup barriers before reading the stage it fills.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
+  // one wait state between the M0 write and the LDS DMA that reads it
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds_base)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
 // XOR swizzle of the four 16-byte chunks of a 64-byte LDS row: conflict-free
 // ds_read_b128 when lanes 0..31 read 32 consecutive rows at one chunk.
