@@ -178,9 +178,9 @@ __global__ __launch_bounds__(WM * WN * 64) void w8a8_gemm_kernel(
 // bank-conflict free.  Requires k % 16 == 0 and 16-byte aligned operands;
 // 16-byte chunks past k are read from a zero block.
 // ---------------------------------------------------------------------------
-template <int WM_, int WN_>
+template <int WM_, int WN_, int STAGES_ = 4>
 struct RingShape {
-  static constexpr int BM = 256, BN = 256, BK = 64, STAGES = 4;
+  static constexpr int BM = 256, BN = 256, BK = 64, STAGES = STAGES_;
   static constexpr int WM = WM_, WN = WN_, NT = WM * WN * 64;
   static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
   static constexpr int ROWS = BM + BN;                      // rows per stage (A then B)
@@ -282,12 +282,7 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
   // passed the barrier.  `issued` is the last stage issued so far.
   auto wait_stage = [&](int t, int issued) {
     const int later = (issued < ktiles - 1 ? issued : ktiles - 1) - t;
-    if (later >= 2)
-      wait_vmcnt<2 * DMA_PER_WAVE>();
-    else if (later == 1)
-      wait_vmcnt<DMA_PER_WAVE>();
-    else
-      wait_vmcnt<0>();
+    wait_stages_after<DMA_PER_WAVE, STAGES - 2>(later);
   };
 
 #pragma unroll

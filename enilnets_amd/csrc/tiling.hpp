@@ -63,6 +63,21 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Waits until at most `later` * per_stage vector-memory operations are in
+// flight, for a wave that issues `per_stage` loads per pipeline stage and has
+// issued `later` (0 .. MAX) stages after the one it needs.
+template <int PER_STAGE, int MAX>
+__device__ __forceinline__ void wait_stages_after(int later) {
+  if constexpr (MAX == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (later >= MAX)
+      wait_vmcnt<MAX * PER_STAGE>();
+    else
+      wait_stages_after<PER_STAGE, MAX - 1>(later);
+  }
+}
+
 __device__ __forceinline__ void wait_lgkmcnt0() {
   __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
 }
