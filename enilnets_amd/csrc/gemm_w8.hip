@@ -126,71 +126,178 @@ __device__ __forceinline__ void split8(const float (&v)[8], Pack8& hi, Pack8& lo
 // the chunk (16x16x32 bf16, x as the A operand) takes k offsets
 // gemv_koff(g, i) + [0, 8).  Both kernels write fp32 partial sums per K
 // slice, part[slice][row][n], which gemv_finish_kernel adds up with the
-// scale, bias and activation.
+// scale, bias and activation (the skinny kernel applies them itself when
+// there is one slice).
+//
+// Every load of these kernels is issued unconditionally from an address
+// clamped into its array, and out-of-range values are zeroed where they are
+// used.  A branch around a load whose other arm writes zeros into the same
+// registers makes the compiler wait for the load before the arms rejoin,
+// which serialises a wave's loads one round trip at a time.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int gemv_koff(int g, int i) { return 64 * (i >> 1) + 16 * g + 8 * (i & 1); }
 
 constexpr int kGemvWaves = 8;
 constexpr int kGemvChunk = 128;
+// 16-column blocks per wave of the decode GEMV: two halve the activation
+// re-reads but measured slower at M = 16, N = K = 8192 (23.4 against 21.0 us
+// for the kernel), one workgroup per CU instead of two
+constexpr int kDecodeCB = 1;
 // outputs this narrow go through the GEMV even for many rows: a GEMM tile
 // grid over them has too few workgroups to stream the activations
 constexpr int64_t kSkinnyN = 32;
 
-// Decode GEMV (m <= 64): grid (groups of 8 x 16 columns, K slices of kr).
-// The workgroup splits its activation slice x[0:16 MB, k0:k0+kr] into bf16
-// planes in LDS once (rows padded by 32 bytes against bank conflicts); each wave then owns 16 columns over the whole slice, issues all its
-// weight loads before the first MFMA, and needs no cross-wave sum.
-template <int MB, int PLANES, int KMODE, int CHUNKS>
-__global__ __launch_bounds__(512) void gemv_decode_kernel(const float* __restrict__ x, int64_t m,
-                                                          int64_t k, int vec,
-                                                          const int8_t* __restrict__ w, int64_t n,
-                                                          int kr, float* __restrict__ part) {
+// 16 codes of row `row` from column k0, loaded without a guard branch: for
+// KMODE 1 a piece past k reads the row's last piece instead (zeroed later by
+// mask_codes16); KMODE 2 keeps the byte-wise guarded load.
+template <int KMODE>
+__device__ __forceinline__ int4 load_codes16_raw(const int8_t* __restrict__ w, int64_t ldw,
+                                                 int64_t row, int64_t k0, int64_t k) {
+  if constexpr (KMODE == 2) {
+    return load_codes16<2>(w, ldw, row, k0, k);
+  } else {
+    const int64_t kk = (KMODE == 0 || k0 < k) ? k0 : k - 16;
+    return *reinterpret_cast<const int4*>(w + row * ldw + kk);
+  }
+}
+
+template <int KMODE>
+__device__ __forceinline__ int4 mask_codes16(int4 v, int64_t k0, int64_t k) {
+  if constexpr (KMODE == 1) return k0 < k ? v : make_int4(0, 0, 0, 0);
+  return v;
+}
+
+// Eight consecutive activations x[row, k0:k0+8] as two float4 loads from
+// clamped addresses (k % 4 == 0 and 16-byte aligned rows), and their
+// zero-masked values once loaded.
+__device__ __forceinline__ void load_row8_raw(const float* __restrict__ x, int64_t row, int64_t m,
+                                              int64_t k, int64_t k0, float4 (&r)[2]) {
+  const float* p = x + (row < m ? row : m - 1) * k;
+  r[0] = *reinterpret_cast<const float4*>(p + (k0 < k ? k0 : 0));
+  r[1] = *reinterpret_cast<const float4*>(p + (k0 + 4 < k ? k0 + 4 : 0));
+}
+
+__device__ __forceinline__ void row8_values(const float4 (&r)[2], int64_t row, int64_t m,
+                                            int64_t k, int64_t k0, float (&v)[8]) {
+  const bool a = row < m && k0 < k, b = row < m && k0 + 4 < k;
+  v[0] = a ? r[0].x : 0.f; v[1] = a ? r[0].y : 0.f; v[2] = a ? r[0].z : 0.f; v[3] = a ? r[0].w : 0.f;
+  v[4] = b ? r[1].x : 0.f; v[5] = b ? r[1].y : 0.f; v[6] = b ? r[1].z : 0.f; v[7] = b ? r[1].w : 0.f;
+}
+
+// scale, bias and activation of one GEMV output (the finish of one sum)
+__device__ __forceinline__ void gemv_output(float s, int64_t row, int64_t c, int64_t n,
+                                            const float* __restrict__ scale,
+                                            const float* __restrict__ bias, const Epilogue& ep,
+                                            float* __restrict__ y, float* __restrict__ z) {
+  float v = s * scale[c];
+  if (bias) v = v + bias[c];
+  if (z) z[row * n + c] = v;
+  y[row * n + c] = epilogue_out(v, ep);
+}
+
+// Decode GEMV (m <= 64): grid (groups of 8 waves x CB x 16 columns, K slices
+// of kr).  The workgroup splits its activation slice x[0:16 MB, k0:k0+kr]
+// into bf16 planes in LDS once (rows padded by 16 bytes: a row pitch of 16
+// modulo 128 bytes puts the 16-byte fragment reads of 8 consecutive rows on
+// 8 distinct bank groups); each wave then owns CB blocks of 16 columns over
+// the whole slice, so one activation fragment read feeds CB MFMAs.  A wave
+// issues its activation loads, then all its weight loads, and stages the
+// activations while the weights are in flight.
+//
+// With one slice the workgroup writes the outputs; otherwise it writes
+// partial sums, part[slice][row][n], for gemv_finish_kernel.  (Adding the
+// slices up inside the kernel, by the last slice of a column group to finish,
+// needs an agent-scope release and acquire per workgroup; on gfx950 those
+// write back and invalidate the whole L2 of the XCD, which measured 3.6x
+// slower than the separate finish pass.)
+template <int MB, int PLANES, int KMODE, int CHUNKS, int CB>
+__global__ __launch_bounds__(512) void gemv_decode_kernel(
+    const float* __restrict__ x, int64_t m, int64_t k, int vec, const int8_t* __restrict__ w,
+    int64_t n, int kr, int splits, float* __restrict__ part,
+    const float* __restrict__ scale, const float* __restrict__ bias, Epilogue ep,
+    float* __restrict__ y, float* __restrict__ z) {
   extern __shared__ __align__(16) uint16_t xs[];
   constexpr int ROWS = 16 * MB;
-  const int pitch = kr + 16;  // bf16 elements per LDS row
+  constexpr int COLS = kGemvWaves * CB * 16;  // columns of a workgroup
+  // ROWS x kr / 8 staging items <= 16 x 1024 / 8 = ITEMS per thread x 512
+  constexpr int ITEMS = 4;
+  const int pitch = kr + 8;  // bf16 elements per LDS row
   const int64_t k0 = int64_t(blockIdx.y) * kr;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, grp = lane >> 4;
-  const int64_t n0 = (int64_t(blockIdx.x) * kGemvWaves + wave) * 16;
+  const int64_t c0 = int64_t(blockIdx.x) * COLS;
+  const int64_t n0 = c0 + int64_t(wave) * CB * 16;  // first column of this wave
   const bool active = n0 < n;
-  const int64_t wrow = n0 + col < n ? n0 + col : n - 1;
   const int64_t k_end = k0 + kr < k ? k0 + kr : k;
-  const int nchunks = int((k_end - k0 + kGemvChunk - 1) / kGemvChunk);
-  // the weight loads go out first: they do not depend on the activations,
-  // so their latency overlaps the staging below
-  int4 wc[CHUNKS][2];
+  const int nchunks = int((k_end - k0 + kGemvChunk - 1) / kGemvChunk);  // >= 1
+  const int groups8 = kr / 8, items = ROWS * groups8;
+
+  float4 xr[ITEMS][2];
+  if (vec) {
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int64_t kc = k0 + int64_t(c) * kGemvChunk + 16 * grp;
-    if (active && c < nchunks) {
-      wc[c][0] = load_codes16<KMODE>(w, k, wrow, kc, k);
-      wc[c][1] = load_codes16<KMODE>(w, k, wrow, kc + 64, k);
-    } else {
-      wc[c][0] = make_int4(0, 0, 0, 0);
-      wc[c][1] = make_int4(0, 0, 0, 0);
+    for (int it = 0; it < ITEMS; ++it) {
+      const int idx = threadIdx.x + it * 512;
+      const int r = idx < items ? idx / groups8 : 0;
+      const int c8 = idx < items ? (idx - r * groups8) * 8 : 0;
+      load_row8_raw(x, r, m, k, k0 + c8, xr[it]);
     }
   }
-  const int groups8 = kr / 8;
-  for (int idx = threadIdx.x; idx < ROWS * groups8; idx += 512) {
-    const int r = idx / groups8, c8 = (idx - r * groups8) * 8;
-    float v[8];
-    load_row8(x, r, m, k, k0 + c8, vec != 0, v);
-    Pack8 hi, lo;
-    split8<PLANES>(v, hi, lo);
-    *reinterpret_cast<Pack8*>(xs + r * pitch + c8) = hi;
-    if (PLANES == 2) *reinterpret_cast<Pack8*>(xs + (ROWS + r) * pitch + c8) = lo;
+  int4 wc[CB][CHUNKS][2];
+#pragma unroll
+  for (int b = 0; b < CB; ++b) {
+    int64_t wrow = n0 + b * 16 + col;
+    wrow = wrow < n ? wrow : n - 1;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      // chunks past the slice re-read its last chunk; their MFMAs are skipped
+      const int cc = c < nchunks ? c : nchunks - 1;
+      const int64_t kc = k0 + int64_t(cc) * kGemvChunk + 16 * grp;
+      wc[b][c][0] = load_codes16_raw<KMODE>(w, k, wrow, kc, k);
+      wc[b][c][1] = load_codes16_raw<KMODE>(w, k, wrow, kc + 64, k);
+    }
+  }
+  if (vec) {
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int idx = threadIdx.x + it * 512;
+      if (idx < items) {
+        const int r = idx / groups8, c8 = (idx - r * groups8) * 8;
+        float v[8];
+        row8_values(xr[it], r, m, k, k0 + c8, v);
+        Pack8 hi, lo;
+        split8<PLANES>(v, hi, lo);
+        *reinterpret_cast<Pack8*>(xs + r * pitch + c8) = hi;
+        if (PLANES == 2) *reinterpret_cast<Pack8*>(xs + (ROWS + r) * pitch + c8) = lo;
+      }
+    }
+  } else {
+    for (int idx = threadIdx.x; idx < items; idx += 512) {
+      const int r = idx / groups8, c8 = (idx - r * groups8) * 8;
+      float v[8];
+      load_row8(x, r, m, k, k0 + c8, false, v);
+      Pack8 hi, lo;
+      split8<PLANES>(v, hi, lo);
+      *reinterpret_cast<Pack8*>(xs + r * pitch + c8) = hi;
+      if (PLANES == 2) *reinterpret_cast<Pack8*>(xs + (ROWS + r) * pitch + c8) = lo;
+    }
   }
   __syncthreads();
   if (!active) return;  // no barrier follows
-  floatx4 acc[MB];
+  floatx4 acc[CB][MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < CB; ++b)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[b][mb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     if (c >= nchunks) break;
-    bf16x8 wb[4];
-    codes16_to_bf16(wc[c][0], wb[0], wb[1]);
-    codes16_to_bf16(wc[c][1], wb[2], wb[3]);
+    const int64_t kc = k0 + int64_t(c) * kGemvChunk + 16 * grp;
+    bf16x8 wb[CB][4];
+#pragma unroll
+    for (int b = 0; b < CB; ++b) {
+      codes16_to_bf16(mask_codes16<KMODE>(wc[b][c][0], kc, k), wb[b][0], wb[b][1]);
+      codes16_to_bf16(mask_codes16<KMODE>(wc[b][c][1], kc + 64, k), wb[b][2], wb[b][3]);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -199,29 +306,42 @@ __global__ __launch_bounds__(512) void gemv_decode_kernel(const float* __restric
         for (int p = 0; p < PLANES; ++p) {
           const bf16x8 xf = *reinterpret_cast<const bf16x8*>(
               xs + (p * ROWS + mb * 16 + col) * pitch + c * kGemvChunk + gemv_koff(grp, i));
-          acc[mb] = mfma_16x16x32_bf16(xf, wb[i], acc[mb]);
+#pragma unroll
+          for (int b = 0; b < CB; ++b) acc[b][mb] = mfma_16x16x32_bf16(xf, wb[b][i], acc[b][mb]);
         }
   }
   // 16x16 output layout: lane holds column l % 16, rows 4 * (l / 16) + r
-  if (n0 + col < n) {
+#pragma unroll
+  for (int b = 0; b < CB; ++b) {
+    const int64_t cn = n0 + b * 16 + col;
+    if (cn >= n) continue;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        part[(int64_t(blockIdx.y) * ROWS + mb * 16 + 4 * grp + r) * n + n0 + col] = acc[mb][r];
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = mb * 16 + 4 * grp + r;
+        if (splits == 1) {
+          if (row < m) gemv_output(0.f + acc[b][mb][r], row, cn, n, scale, bias, ep, y, z);
+        } else {
+          part[(int64_t(blockIdx.y) * ROWS + row) * n + cn] = acc[b][mb][r];
+        }
+      }
   }
 }
 
 // Tall-skinny GEMV (n <= 32, any m): grid (column groups, K splits, 16-row
 // blocks).  Each wave owns a K range of `chunks` x 128 and keeps the
 // activation fragments of its rows in registers, read from fp32 and split
-// there; it then streams 16-column blocks of W, and the 8 waves' partial
-// tiles are summed through LDS.
+// there; it then streams 16-column blocks of W (the next block's loads in
+// flight while one is multiplied), and the 8 waves' partial tiles are summed
+// through LDS.  With one K split (part == nullptr) the kernel finishes the
+// outputs itself.
 template <int PLANES, int KMODE>
 __global__ __launch_bounds__(512) void gemv_skinny_kernel(
     const float* __restrict__ x, int64_t m, int64_t k, int vec, const int8_t* __restrict__ w,
     int64_t n, int chunks_per_wave, int col_blocks_per_group, int64_t mp,
-    float* __restrict__ part) {
+    float* __restrict__ part, const float* __restrict__ scale, const float* __restrict__ bias,
+    Epilogue ep, float* __restrict__ y, float* __restrict__ z) {
   constexpr int CHUNKS = 2;
   __shared__ float red[kGemvWaves][16][17];
   const int lane = threadIdx.x & 63;
@@ -230,6 +350,35 @@ __global__ __launch_bounds__(512) void gemv_skinny_kernel(
   const int grp = lane >> 4;
   const int64_t k_wave0 = (int64_t(blockIdx.y) * kGemvWaves + wave) * chunks_per_wave * kGemvChunk;
   const int64_t row0 = int64_t(blockIdx.z) * 16;
+  const int64_t xrow = row0 + col;
+
+  // activation loads first, then the first block's weights
+  float4 xr[CHUNKS][4][2];
+  if (vec) {
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        load_row8_raw(x, xrow, m, k, k_wave0 + int64_t(c) * kGemvChunk + gemv_koff(grp, i),
+                      xr[c][i]);
+  }
+  auto load_block = [&](int cb, int4 (&wc)[CHUNKS][2]) {
+    int64_t nb = (int64_t(blockIdx.x) * col_blocks_per_group + cb) * 16 + col;
+    nb = nb < n ? nb : n - 1;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      // a chunk past k re-reads valid codes (KMODE 0, k % 128 == 0: the
+      // last chunk; otherwise the loader clamps each piece); they are zeroed
+      // below
+      int64_t kb = k_wave0 + int64_t(c) * kGemvChunk;
+      if (KMODE == 0) kb = kb < k ? kb : k - kGemvChunk;
+      const int64_t kc = kb + 16 * grp;
+      wc[c][0] = load_codes16_raw<KMODE>(w, k, nb, kc, k);
+      wc[c][1] = load_codes16_raw<KMODE>(w, k, nb, kc + 64, k);
+    }
+  };
+  int4 wc[CHUNKS][2], wn[CHUNKS][2];
+  load_block(0, wc);
 
   bf16x8 xf[CHUNKS][PLANES][4];
 #pragma unroll
@@ -239,7 +388,10 @@ __global__ __launch_bounds__(512) void gemv_skinny_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float v[8];
-      load_row8(x, live ? row0 + col : m, m, k, kc + gemv_koff(grp, i), vec != 0, v);
+      if (vec)
+        row8_values(xr[c][i], live ? xrow : m, m, k, kc + gemv_koff(grp, i), v);
+      else
+        load_row8(x, live ? xrow : m, m, k, kc + gemv_koff(grp, i), false, v);
       Pack8 hi, lo;
       split8<PLANES>(v, hi, lo);
       xf[c][0][i] = __builtin_bit_cast(bf16x8, hi);
@@ -250,26 +402,18 @@ __global__ __launch_bounds__(512) void gemv_skinny_kernel(
   for (int cb = 0; cb < col_blocks_per_group; ++cb) {
     const int64_t n0 = (int64_t(blockIdx.x) * col_blocks_per_group + cb) * 16;
     if (n0 >= n) break;
-    const int64_t row = n0 + col < n ? n0 + col : n - 1;
-    int4 wc[CHUNKS][2];
-#pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-      const int64_t kbase = k_wave0 + int64_t(c) * kGemvChunk;
-      const int64_t kc = kbase + 16 * grp;
-      if (c < chunks_per_wave && kbase < k) {
-        wc[c][0] = load_codes16<KMODE>(w, k, row, kc, k);
-        wc[c][1] = load_codes16<KMODE>(w, k, row, kc + 64, k);
-      } else {
-        wc[c][0] = make_int4(0, 0, 0, 0);
-        wc[c][1] = make_int4(0, 0, 0, 0);
-      }
-    }
+    const bool next = cb + 1 < col_blocks_per_group && n0 + 16 < n;
+    if (next) load_block(cb + 1, wn);
     floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c) {
+      const int64_t kbase = k_wave0 + int64_t(c) * kGemvChunk;
+      const bool live = c < chunks_per_wave && kbase < k;
+      const int64_t kc = kbase + 16 * grp;
+      const int4 z4 = make_int4(0, 0, 0, 0);
       bf16x8 wb[4];
-      codes16_to_bf16(wc[c][0], wb[0], wb[1]);
-      codes16_to_bf16(wc[c][1], wb[2], wb[3]);
+      codes16_to_bf16(live ? mask_codes16<KMODE>(wc[c][0], kc, k) : z4, wb[0], wb[1]);
+      codes16_to_bf16(live ? mask_codes16<KMODE>(wc[c][1], kc + 64, k) : z4, wb[2], wb[3]);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -283,9 +427,21 @@ __global__ __launch_bounds__(512) void gemv_skinny_kernel(
       float s = 0.f;
 #pragma unroll
       for (int v = 0; v < kGemvWaves; ++v) s += red[v][mm][nn];
-      if (n0 + nn < n) part[(int64_t(blockIdx.y) * mp + row0 + mm) * n + n0 + nn] = s;
+      if (n0 + nn < n) {
+        if (part)
+          part[(int64_t(blockIdx.y) * mp + row0 + mm) * n + n0 + nn] = s;
+        else if (row0 + mm < m)
+          gemv_output(0.f + s, row0 + mm, n0 + nn, n, scale, bias, ep, y, z);
+      }
     }
     __syncthreads();
+    if (next) {
+#pragma unroll
+      for (int c = 0; c < CHUNKS; ++c) {
+        wc[c][0] = wn[c][0];
+        wc[c][1] = wn[c][1];
+      }
+    }
   }
 }
 
@@ -298,12 +454,20 @@ __global__ __launch_bounds__(256) void gemv_finish_kernel(const float* __restric
   const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= m * n) return;
   const int64_t row = idx / n, c = idx - row * n;
+  const float* p = part + row * n + c;
+  const int64_t stride = mp * n;
+  // eight slices' loads in flight at a time; the sum keeps slice order
   float s = 0.f;
-  for (int sp = 0; sp < splits; ++sp) s += part[(int64_t(sp) * mp + row) * n + c];
-  float v = s * scale[c];
-  if (bias) v = v + bias[c];
-  if (z) z[idx] = v;
-  y[idx] = epilogue_out(v, ep);
+  int sp = 0;
+  for (; sp + 8 <= splits; sp += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = p[int64_t(sp + j) * stride];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += v[j];
+  }
+  for (; sp < splits; ++sp) s += p[int64_t(sp) * stride];
+  gemv_output(s, row, c, n, scale, bias, ep, y, z);
 }
 
 // ---------------------------------------------------------------------------
@@ -832,7 +996,9 @@ struct GemvPlan {
   int kr;            // decode: K slice per workgroup (multiple of 128)
   int chunks_per_wave, cb_per_group;  // skinny
   int64_t groups, splits, m_blocks, mp;
-  size_t part_bytes(int64_t n) const { return sizeof(float) * size_t(splits * mp * n); }
+  size_t part_bytes(int64_t n) const {
+    return splits > 1 ? sizeof(float) * size_t(splits * mp * n) : 0;
+  }
 };
 
 GemvPlan plan_gemv(int64_t m, int64_t n, int64_t k) {
@@ -843,7 +1009,7 @@ GemvPlan plan_gemv(int64_t m, int64_t n, int64_t k) {
     g.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
     g.m_blocks = 1;
     g.mp = 16 * g.mb;
-    g.groups = ceil_div(n, 16 * kGemvWaves);
+    g.groups = ceil_div(n, 16 * kGemvWaves * kDecodeCB);
     // the longest slice the LDS copy allows (16 MB rows x kr <= 16 x 1024),
     // shortened until groups x splits fill the device twice over
     const int64_t kr_max = 1024 / g.mb;
@@ -872,18 +1038,19 @@ GemvPlan plan_gemv(int64_t m, int64_t n, int64_t k) {
 
 template <int MB, int PLANES, int KMODE>
 void launch_decode(const GemvPlan& g, const float* x, int64_t m, int64_t k, int vec,
-                   const int8_t* w, int64_t n, float* part) {
+                   const int8_t* w, int64_t n, float* part, const float* scale,
+                   const float* bias, const Epilogue& ep, float* y, float* z) {
   constexpr int CHUNKS = 8 / MB;  // kr <= 1024 / MB
-  const size_t lds = size_t(PLANES) * 16 * MB * (g.kr + 16) * sizeof(uint16_t);
-  auto kernel = gemv_decode_kernel<MB, PLANES, KMODE, CHUNKS>;
+  const size_t lds = size_t(PLANES) * 16 * MB * (g.kr + 8) * sizeof(uint16_t);
+  auto kernel = gemv_decode_kernel<MB, PLANES, KMODE, CHUNKS, kDecodeCB>;
   static bool attr_set = false;
   if (!attr_set) {
     ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024));
     attr_set = true;
   }
-  kernel<<<dim3(unsigned(g.groups), unsigned(g.splits)), 512, lds, stream()>>>(x, m, k, vec, w, n,
-                                                                            g.kr, part);
+  kernel<<<dim3(unsigned(g.groups), unsigned(g.splits)), 512, lds, stream()>>>(
+      x, m, k, vec, w, n, g.kr, int(g.splits), part, scale, bias, ep, y, z);
   check_launch("gemv_decode_kernel");
 }
 
@@ -894,16 +1061,21 @@ void gemv_dispatch(const GemvPlan& g, const float* x, const int8_t* w, const flo
   const int vec = (k % 4 == 0) && aligned(x, 16);
   if (g.decode) {
     if (g.mb == 1)
-      launch_decode<1, PLANES, KMODE>(g, x, m, k, vec, w, n, part);
+      launch_decode<1, PLANES, KMODE>(g, x, m, k, vec, w, n, part, scale, bias, ep, y, z);
     else if (g.mb == 2)
-      launch_decode<2, PLANES, KMODE>(g, x, m, k, vec, w, n, part);
+      launch_decode<2, PLANES, KMODE>(g, x, m, k, vec, w, n, part, scale, bias, ep, y, z);
     else
-      launch_decode<4, PLANES, KMODE>(g, x, m, k, vec, w, n, part);
+      launch_decode<4, PLANES, KMODE>(g, x, m, k, vec, w, n, part, scale, bias, ep, y, z);
+    if (g.splits == 1) return;
   } else {
+    // one K split: the kernel finishes the outputs itself
+    const bool direct = g.splits == 1;
     gemv_skinny_kernel<PLANES, KMODE>
         <<<dim3(unsigned(g.groups), unsigned(g.splits), unsigned(g.m_blocks)), 512, 0,
-           stream()>>>(x, m, k, vec, w, n, g.chunks_per_wave, g.cb_per_group, g.mp, part);
+           stream()>>>(x, m, k, vec, w, n, g.chunks_per_wave, g.cb_per_group, g.mp,
+                       direct ? nullptr : part, scale, bias, ep, y, z);
     check_launch("gemv_skinny_kernel");
+    if (direct) return;
   }
   gemv_finish_kernel<<<unsigned(ceil_div(m * n, 256)), 256, 0, stream()>>>(
       part, int(g.splits), g.mp, m, n, scale, bias, ep, y, z);
