@@ -659,8 +659,8 @@ struct RingCfg {
   static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole 1 KiB blocks");
   static constexpr int LDS_BYTES = STAGES * STAGE_BYTES + 2 * BCONV_BYTES + 2 * ACONV_BYTES;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-  static_assert(NT >= 2 * BN, "one expansion item per thread");
-  static_assert(!FUSED_A || NT >= 4 * BM, "one split item per thread");
+  static_assert((4 * BN) % NT == 0, "whole 8-code expansion items per thread");
+  static_assert(!FUSED_A || (4 * BM) % NT == 0, "whole split items per thread");
 };
 
 __device__ __forceinline__ int swz32(int row, int half) { return half ^ ((row >> 3) & 1); }
@@ -790,52 +790,58 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) b_off[j][ks] = r * 64 + 16 * swz64(r, 2 * g + ks);
   }
-  // conversion item of this thread: 16 codes of B row cr, k half ch, which
-  // become logical 16-byte chunks 2 ch and 2 ch + 1 of the bf16 row
-  const bool converts = tid < BN * 2;
-  const int cr = tid >> 1, ch = tid & 1;
-  const int conv_src = C::A_BYTES + cr * 32 + 16 * swz32(cr, ch);
-  const int conv_dst0 = cr * 64 + 16 * swz64(cr, 2 * ch);
-  const int conv_dst1 = cr * 64 + 16 * swz64(cr, 2 * ch + 1);
-  // fused split item of this thread: 8 floats (logical chunks 2 ag and
-  // 2 ag + 1) of A row ar, which become chunk ag of that row in each plane
-  const bool splits = C::FUSED_A && tid < 4 * BM;
-  const int ar = tid >> 2, ag = tid & 3;
-  const int split_src0 = ar * 128 + 16 * swz128(ar, 2 * ag);
-  const int split_src1 = ar * 128 + 16 * swz128(ar, 2 * ag + 1);
-  const int split_dst = ar * 64 + 16 * swz64(ar, ag);
+  // Expansion items, every thread the same number so that no branch splits
+  // the loop body: piece q of 8 codes of B row cr (logical bytes 8 q ..
+  // 8 q + 7 of the 32-code row) becomes logical 16-byte chunk q of the bf16
+  // row; fused split item a: 8 floats (logical chunks 2 ag and 2 ag + 1) of
+  // A row ar, which become chunk ag of that row in each plane.
+  constexpr int B_ITEMS = 4 * BN / C::NT;
+  constexpr int A_ITEMS = C::FUSED_A ? 4 * BM / C::NT : 0;
+  constexpr int A_SLOTS = A_ITEMS > 0 ? A_ITEMS : 1;
+  int conv_src[B_ITEMS], conv_dst[B_ITEMS];
+#pragma unroll
+  for (int it = 0; it < B_ITEMS; ++it) {
+    const int item = tid + it * C::NT, cr = item >> 2, q = item & 3;
+    conv_src[it] = C::A_BYTES + cr * 32 + 16 * swz32(cr, q >> 1) + 8 * (q & 1);
+    conv_dst[it] = cr * 64 + 16 * swz64(cr, q);
+  }
+  int split_src0[A_SLOTS], split_src1[A_SLOTS], split_dst[A_SLOTS];
+#pragma unroll
+  for (int it = 0; it < A_SLOTS; ++it) {
+    const int item = tid + it * C::NT, ar = item >> 2, ag = item & 3;
+    split_src0[it] = ar * 128 + 16 * swz128(ar, 2 * ag);
+    split_src1[it] = ar * 128 + 16 * swz128(ar, 2 * ag + 1);
+    split_dst[it] = ar * 64 + 16 * swz64(ar, ag);
+  }
   // expansion of stage t in two halves: the LDS reads, issued beside the
-  // fragment reads, and the conversion and LDS writes, issued after the
-  // MFMAs so that they run while the MFMAs execute
-  int4 craw = make_int4(0, 0, 0, 0);
-  float4 sa = make_float4(0.f, 0.f, 0.f, 0.f), sb = sa;
+  // fragment reads, and the conversion and LDS writes, scheduled among the
+  // MFMAs so that they issue while the MFMAs execute
+  uint2 craw[B_ITEMS];
+  float4 sa[A_SLOTS], sb[A_SLOTS];
   auto convert_load = [&](int t) {
     const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
-    if (converts) craw = *reinterpret_cast<const int4*>(st + conv_src);
-    if constexpr (C::FUSED_A) {
-      if (splits) {
-        sa = *reinterpret_cast<const float4*>(st + split_src0);
-        sb = *reinterpret_cast<const float4*>(st + split_src1);
-      }
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) craw[it] = *reinterpret_cast<const uint2*>(st + conv_src[it]);
+#pragma unroll
+    for (int it = 0; it < A_ITEMS; ++it) {
+      sa[it] = *reinterpret_cast<const float4*>(st + split_src0[it]);
+      sb[it] = *reinterpret_cast<const float4*>(st + split_src1[it]);
     }
   };
   auto convert_store = [&](int t) {
-    if (converts) {
-      bf16x8 first, second;
-      codes16_to_bf16(craw, first, second);
-      char* dst = bconv + (t & 1) * C::BCONV_BYTES;
-      *reinterpret_cast<bf16x8*>(dst + conv_dst0) = first;
-      *reinterpret_cast<bf16x8*>(dst + conv_dst1) = second;
-    }
-    if constexpr (C::FUSED_A) {
-      if (splits) {
-        const float v[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
-        Pack8 hi, lo;
-        split8<PLANES>(v, hi, lo);
-        char* dst = aconv + (t & 1) * C::ACONV_BYTES;
-        *reinterpret_cast<Pack8*>(dst + split_dst) = hi;
-        if (PLANES == 2) *reinterpret_cast<Pack8*>(dst + BM * 64 + split_dst) = lo;
-      }
+    char* bdst = bconv + (t & 1) * C::BCONV_BYTES;
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it)
+      *reinterpret_cast<bf16x8*>(bdst + conv_dst[it]) = codes8_to_bf16(craw[it].x, craw[it].y);
+    char* adst = aconv + (t & 1) * C::ACONV_BYTES;
+#pragma unroll
+    for (int it = 0; it < A_ITEMS; ++it) {
+      const float v[8] = {sa[it].x, sa[it].y, sa[it].z, sa[it].w,
+                          sb[it].x, sb[it].y, sb[it].z, sb[it].w};
+      Pack8 hi, lo;
+      split8<PLANES>(v, hi, lo);
+      *reinterpret_cast<Pack8*>(adst + split_dst[it]) = hi;
+      if (PLANES == 2) *reinterpret_cast<Pack8*>(adst + BM * 64 + split_dst[it]) = lo;
     }
   };
   bf16x8 fa[PLANES][FM][2], fb[FN][2];
@@ -875,9 +881,11 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
     wait_lgkmcnt0();  // this wave's expansion writes of stage t are done
     block_barrier();
     if (t + STAGES - 1 < ktiles) issue(t + STAGES - 1);
+    // the raw tile of stage t + 1 first, so that its conversion can issue
+    // among stage t's MFMAs; the last iteration expands a stage past the
+    // end into the buffer no one reads again (no branch in the body)
+    convert_load(t + 1);
     read_frags(t);
-    if (t + 1 < ktiles) convert_load(t + 1);
-    sched_fence();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -887,8 +895,8 @@ __global__ __launch_bounds__(C::NT, 1) void w8_ring_kernel(
 #pragma unroll
           for (int p = 0; p < PLANES; ++p)
             acc[i][j] = mfma_32x32x16_bf16(fa[p][i][ks], fb[j][ks], acc[i][j]);
+    convert_store(t + 1);
     sched_fence();
-    if (t + 1 < ktiles) convert_store(t + 1);
   }
 
   const int lhalf = lane >> 5;

@@ -67,6 +67,14 @@ __device__ __forceinline__ void codes4_to_bf16(uint32_t word, uint32_t& lo_pair,
   hi_pair = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
 }
 
+// 8 int8 codes -> 8 bf16.
+__device__ __forceinline__ bf16x8 codes8_to_bf16(uint32_t lo, uint32_t hi) {
+  uint32_t d[4];
+  codes4_to_bf16(lo, d[0], d[1]);
+  codes4_to_bf16(hi, d[2], d[3]);
+  return __builtin_bit_cast(bf16x8, d);
+}
+
 // 16 int8 codes -> two groups of 8 bf16 (codes 0..7 and 8..15).
 __device__ __forceinline__ void codes16_to_bf16(int4 raw, bf16x8& first, bf16x8& second) {
   uint32_t d[8];
