@@ -14,7 +14,8 @@ algorithmic TFLOP/s (2 * M * sum(N * K)).
 quantize / dequantize GB/s, the M=16 GEMV, the M=4096 W8 GEMM in both
 variants, per-token activation quantization and the W8A8 int8 GEMM at
 M=4096 and 8192^3.  Memory-bound kernels rotate over enough buffers to
-exceed the 256 MB MALL, so their bytes come from HBM.
+exceed the 256 MB MALL, so their bytes come from HBM.  bench_vendor.py times
+the vendor library on the same GEMM shapes as a reference point.
 
 ``roofline`` is the dominant kernel of the headline step (the largest MLP
 layer's W8 GEMM), timed with HIP events on the library stream.
