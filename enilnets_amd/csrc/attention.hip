@@ -42,12 +42,23 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
   __shared__ float red[4];
   const float* xr = x + int64_t(blockIdx.x) * cols;
   float* yr = y + int64_t(blockIdx.x) * cols;
-  float v[PER];
+  // the row, gamma and beta are all loaded up front from in-bounds
+  // addresses and masked afterwards, so the loads are in flight together
+  // (loads inside the guarded store blocks were each waited on in turn)
+  float v[PER], gm[PER], bt[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t c = int64_t(i) * 256 + threadIdx.x;
+    const int64_t cc = c < cols ? c : 0;
+    v[i] = xr[cc];
+    gm[i] = gamma[cc];
+    bt[i] = beta[cc];
+  }
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int64_t c = int64_t(i) * 256 + threadIdx.x;
-    v[i] = c < cols ? xr[c] : 0.0f;
+    v[i] = c < cols ? v[i] : 0.0f;
     s += v[i];
   }
   const float mean = block_sum256(s, red) / float(cols);
@@ -63,7 +74,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int64_t c = int64_t(i) * 256 + threadIdx.x;
-    if (c < cols) yr[c] = gamma[c] * ((v[i] - mean) / den) + beta[c];
+    if (c < cols) yr[c] = gm[i] * ((v[i] - mean) / den) + bt[i];
   }
 }
 

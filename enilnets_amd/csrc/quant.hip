@@ -227,19 +227,24 @@ __global__ __launch_bounds__(TPR < kBlock ? kBlock : TPR) void rows_quant_kernel
   const int t = threadIdx.x % TPR;
   const int64_t row = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
   const bool active = row < rows;
-  const T* src = w + row * cols;
+  const T* src = w + (active ? row : 0) * cols;
 
+  // every chunk is loaded from an in-bounds address and zeroed afterwards if
+  // it lies outside the row: a load behind a guard branch whose other arm
+  // writes zeros makes the compiler wait for it before the next chunk's load
   T vals[CHUNKS][V];
+  {
+    Vec<T, V> raw[CHUNKS];
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int64_t idx = (int64_t(c) * TPR + t) * V;
-    if (active && idx < cols) {
-      Vec<T, V> v = load_vec<T, V>(src + idx);
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int64_t idx = (int64_t(c) * TPR + t) * V;
+      raw[c] = load_vec<T, V>(src + (idx < cols ? idx : 0));
+    }
 #pragma unroll
-      for (int e = 0; e < V; ++e) vals[c][e] = v.v[e];
-    } else {
+    for (int c = 0; c < CHUNKS; ++c) {
+      const bool live = active && (int64_t(c) * TPR + t) * V < cols;
 #pragma unroll
-      for (int e = 0; e < V; ++e) vals[c][e] = T(0);
+      for (int e = 0; e < V; ++e) vals[c][e] = live ? raw[c].v[e] : T(0);
     }
   }
   // a: max |x| (SYM) or min x; b: max x (asymmetric only).  Padding zeros do
