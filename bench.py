@@ -226,6 +226,20 @@ def components(timer, rng, only):
             _lib.call("enq_quantize_tensor", _lib.F32, d_ws[j].ptr, 1, N, K, 8, _lib.SYMMETRIC,
                       null(), d_codes[j].ptr, d_scale[j].ptr, d_zp.ptr, null())
 
+    if on("quantize_per_tensor"):
+        # one absmax over the whole tensor, then the quantize pass: the
+        # reference's two passes (statistics, then quantize) read W twice
+        def qt(i):
+            j = i % copies
+            _lib.call("enq_quantize_tensor", _lib.F32, d_ws[j].ptr, 1, 1, nk, 8, _lib.SYMMETRIC,
+                      null(), d_codes[j].ptr, d_scale[j].ptr, d_zp.ptr, null())
+        qt(0)
+        ms = timer.time(qt, 30)
+        nbytes = 2 * 4 * nk + nk + 4
+        out["quantize_8192x8192_per_tensor_int8"] = {
+            "ms": ms, "GB/s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            "bytes": nbytes}
+
     if on("fake_quantize"):
         d_fake = [DeviceArray((N, K), np.float32) for _ in range(2)]
 
