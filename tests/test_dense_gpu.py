@@ -95,6 +95,23 @@ def test_dense_w8_activations(gpu, act):
     assert np.allclose(y, want, rtol=2e-6, atol=2e-6)
 
 
+@pytest.mark.parametrize("m,k,n", [(3, 100, 10), (40, 128, 300), (77, 130, 17), (4096, 1024, 10)])
+@pytest.mark.parametrize("act", ["relu", "gelu", "elu", "softmax"])
+def test_dense_w8_gemv_direct_activations(gpu, m, k, n, act):
+    # GEMV shapes with a single K slice: the decode (m <= 64) and skinny
+    # (n <= 32) kernels apply the scale, bias and activation themselves
+    print(f"[case] gemv direct {act} m={m} k={k} n={n}", flush=True)
+    x, fq, codes, rows, b, wq = make(m, k, n, seed=m + 3 * k + n)
+    z = DeviceArray((m, n), np.float32)
+    y = D.dense_w8(DeviceArray.from_numpy(x), wq, DeviceArray.from_numpy(b), act,
+                   pre_activation=z).numpy()
+    zh = z.numpy()
+    z_ref = x.astype(np.float64) @ fq.astype(np.float64).T + b
+    assert np.all(row_rel_err(zh.astype(np.float64), z_ref) <= 1e-4)
+    want = oracle.activate(act, zh.astype(np.float64))
+    assert np.allclose(y, want, rtol=2e-6, atol=2e-6)
+
+
 def test_dense_w8_rejects_bad_shapes(gpu):
     x, fq, codes, rows, b, wq = make(4, 32, 8, seed=1)
     with pytest.raises(ValueError):
