@@ -327,6 +327,131 @@ def components(timer, rng, only):
         out.update(transformer_block(timer, rng))
     if on("moe"):
         out.update(moe_layer(timer, rng))
+    if on("next_rows"):
+        out.update(next_rows(timer, rng))
+    return out
+
+
+def next_rows(timer, rng):
+    """The rows built beside the hot path: the activation fake-quantization
+    fused into the Dense epilogue, the int8 on-disk format, KV-cache decode
+    and the QAT forward.  Device-resident operations are timed with HIP
+    events on the library stream; the file and the decode step, whose API
+    takes and returns host arrays, with the host clock."""
+    import tempfile
+    from enilnets_amd import quantize_weights
+    from enilnets_amd.device import DeviceArray
+    from enilnets_amd.nn import LoadInt8, Model, SaveInt8, int8_weights
+    from enilnets_amd.nn.dense import act_quant, dense_w8
+    from enilnets_amd.nn.kvcache import KVCache, cached_forward_step
+    from enilnets_amd.nn.qat import QATLinear
+    out = {}
+
+    # activation fake-quantization (a calibrated per-tensor spec, float64
+    # arithmetic as the calibrator's 0-d float64 scale gives) fused into the
+    # epilogue of the MLP's 4096 x 1024 x 1024 layer, against the plain layer
+    # and the standalone pass over the same output
+    M, K, N = 4096, 1024, 1024
+    w = rng.normal(0.0, np.sqrt(2.0 / K), (N, K)).astype(np.float32)
+    m = Model()
+    m.add_dense(w, np.zeros(N, np.float32), "relu")
+    quantize_weights(m, bits=8, per_channel=True)
+    wq = int8_weights(m.layers[0], "weights")
+    x = DeviceArray.from_numpy(rng.uniform(0.0, 1.0, (M, K)).astype(np.float32))
+    y, y2 = DeviceArray((M, N), np.float32), DeviceArray((M, N), np.float32)
+    spec = {"bits": 8, "scheme": "symmetric", "scale": np.array(0.02),
+            "zero_point": np.array(0.0)}
+    dense_w8(x, wq, None, "relu", out=y, act_quant=spec)
+    plain = timer.time(lambda i: dense_w8(x, wq, None, "relu", out=y), 20)
+    fused = timer.time(lambda i: dense_w8(x, wq, None, "relu", out=y, act_quant=spec), 20)
+    alone = timer.time(lambda i: act_quant(y, spec, np.float32, out=y2), 20)
+    out["act_quant_epilogue_4096x1024x1024"] = {
+        "dense_ms": plain, "dense_with_act_quant_ms": fused, "overhead_frac": fused / plain - 1.0,
+        "standalone_pass_ms": alone, "standalone_GB/s": 8.0 * M * N / alone / 1e6}
+
+    # QAT forward: per-step per-channel weight fake-quantization feeding the
+    # W8 Dense (QATLinear.forward, training=False)
+    q = QATLinear(w, np.zeros(N, np.float32))
+    q.forward(x, training=False)
+    ms = timer.time(lambda i: q.forward(x, training=False), 20)
+    out["qat_forward_4096x1024x1024"] = {
+        "ms": ms, "TFLOP/s": 2.0 * M * N * K / ms / 1e9,
+        "note": "weight fake-quant (quantize_tensor per channel) + Dense, per call"}
+    del x, y, y2
+
+    # int8 on-disk format of the 8192 x 8192 weight (BASELINE configs[2])
+    big = Model()
+    big.add_dense(rng.normal(0.0, 0.02, (8192, 8192)).astype(np.float32),
+                  np.zeros(8192, np.float32), "linear")
+    quantize_weights(big, bits=8, per_channel=True)
+    int8_weights(big.layers[0], "weights")
+    with tempfile.TemporaryDirectory() as d:
+        f = os.path.join(d, "w8.npz")
+        t0 = time.perf_counter()
+        info = SaveInt8(big, f)
+        t1 = time.perf_counter()
+        size = os.path.getsize(f)
+        t2 = time.perf_counter()
+        LoadInt8(f)
+        t3 = time.perf_counter()
+    out["int8_file_8192x8192"] = {
+        "save_ms": (t1 - t0) * 1e3, "load_ms": (t3 - t2) * 1e3, "file_bytes": size,
+        "int8_bytes": info["int8_bytes"], "float_bytes": info["float_bytes"],
+        "note": "host clock: npz write / read, codes uploaded and dequantized on the device, "
+                "fake-quantized floats copied back"}
+    del big
+
+    # KV-cache decode: the configs[3] block made causal, batch 8, a 512-token
+    # prompt, then one token per step
+    B, S, E, F, H, steps = 8, 512, 1024, 4096, 16, 32
+    dec = Model()
+    dec.add_residual_start()
+    dec.add_layernorm(E)
+    ws = [rng.normal(0.0, 0.02, (E, E)).astype(np.float32) for _ in range(4)]
+    dec.add_multihead_attention(*ws, num_heads=H, causal=True)
+    dec.add_residual_end()
+    dec.add_residual_start()
+    dec.add_layernorm(E)
+    dec.add_dense(rng.normal(0.0, 0.02, (F, E)).astype(np.float32), np.zeros(F, np.float32), "gelu")
+    dec.add_dense(rng.normal(0.0, 0.02, (E, F)).astype(np.float32), np.zeros(E, np.float32),
+                  "linear")
+    dec.add_residual_end()
+    quantize_weights(dec, bits=8, per_channel=True)
+    prompt = rng.standard_normal((B, S, E)).astype(np.float32)
+    new = rng.standard_normal((B, steps + 2, E)).astype(np.float32)
+    warm = KVCache()
+    cached_forward_step(dec, prompt, warm)
+    cached_forward_step(dec, new[:, :1], warm)
+    cache = KVCache()
+    t0 = time.perf_counter()
+    cached_forward_step(dec, prompt, cache)
+    t1 = time.perf_counter()
+    for i in range(2):
+        cached_forward_step(dec, new[:, i:i + 1], cache)
+    t2 = time.perf_counter()
+    for i in range(2, steps + 2):
+        cached_forward_step(dec, new[:, i:i + 1], cache)
+    t3 = time.perf_counter()
+    step_ms = (t3 - t2) * 1e3 / steps
+    # the same session with KVCache(trust_weights=True): no per-step hash of
+    # every host weight, device weights, biases and buffers kept
+    tcache = KVCache(trust_weights=True)
+    cached_forward_step(dec, prompt, tcache)
+    for i in range(2):
+        cached_forward_step(dec, new[:, i:i + 1], tcache)
+    t4 = time.perf_counter()
+    for i in range(2, steps + 2):
+        cached_forward_step(dec, new[:, i:i + 1], tcache)
+    t5 = time.perf_counter()
+    trusted_ms = (t5 - t4) * 1e3 / steps
+    weight_bytes = 4 * E * E + 2 * E * F
+    out["kv_decode_b8_ctx512_e1024"] = {
+        "prefill_ms": (t1 - t0) * 1e3, "ms_per_step": step_ms, "tokens/s": B / step_ms * 1e3,
+        "ms_per_step_trusted_weights": trusted_ms, "tokens/s_trusted_weights": B / trusted_ms * 1e3,
+        "weight_bytes_per_step": weight_bytes,
+        "kv_bytes_per_step": 2 * B * (S + steps) * E * 4,
+        "note": "host clock per cached_forward_step: host dispatch of every layer, the device "
+                "work and the copy of the new positions' outputs back"}
     return out
 
 

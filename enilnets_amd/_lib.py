@@ -64,6 +64,7 @@ SIGNATURES = {
     "enq_set_stream": (c_int, [_P]),
     "enq_malloc": (c_int, [POINTER(c_void_p), c_size_t]),
     "enq_free": (c_int, [_P]),
+    "enq_release_cached_memory": (c_int, []),
     "enq_copy_to_device": (c_int, [_P, _P, c_size_t]),
     "enq_copy_to_host": (c_int, [_P, _P, c_size_t]),
     "enq_copy_on_device": (c_int, [_P, _P, c_size_t]),

@@ -2,6 +2,8 @@
 #include <cstdarg>
 #include <cstring>
 #include <mutex>
+#include <unordered_map>
+#include <vector>
 
 #include "common.hpp"
 
@@ -23,6 +25,43 @@ struct DeviceState {
 
 DeviceState g_state;
 std::mutex g_mutex;
+
+// Caching device allocator behind enq_malloc / enq_free.  Every kernel and
+// copy of the library runs in order on one stream, so a freed block can be
+// handed out again at once: whatever is enqueued on it next runs after the
+// work that used it before.  Freeing therefore neither synchronises nor
+// calls hipFree; blocks are kept per size class until enq_release_cached_memory
+// (or an allocation that fails) returns them to the device.  Switching the
+// stream (enq_set_stream) first synchronises the old one, which keeps that
+// ordering argument true for the cached blocks.
+struct BlockCache {
+  std::mutex mu;
+  std::unordered_map<void*, size_t> live;                  // block -> size class
+  std::unordered_map<size_t, std::vector<void*>> idle;    // size class -> blocks
+};
+BlockCache g_blocks;
+
+// 256 B .. 1 MiB in powers of two, then multiples of 2 MiB.
+size_t size_class(size_t bytes) {
+  if (bytes <= (size_t(1) << 20)) {
+    size_t c = 256;
+    while (c < bytes) c <<= 1;
+    return c;
+  }
+  const size_t g = size_t(2) << 20;
+  return (bytes + g - 1) / g * g;
+}
+
+// Returns every idle block to the device; the caller holds g_blocks.mu.
+void release_idle_locked() {
+  bool any = false;
+  for (auto& kv : g_blocks.idle) any = any || !kv.second.empty();
+  if (!any) return;
+  ENQ_HIP(hipStreamSynchronize(stream()));
+  for (auto& kv : g_blocks.idle)
+    for (void* p : kv.second) ENQ_HIP(hipFree(p));
+  g_blocks.idle.clear();
+}
 
 }  // namespace
 
@@ -169,6 +208,8 @@ int enq_get_stream(void** s) {
 int enq_set_stream(void* s) {
   return guarded([&] {
     require_init();
+    // cached blocks were last used on the old stream
+    ENQ_HIP(hipStreamSynchronize(stream()));
     g_state.user_stream = static_cast<hipStream_t>(s);
   });
 }
@@ -179,7 +220,20 @@ int enq_malloc(void** dptr, size_t bytes) {
     ENQ_REQUIRE(dptr != nullptr, "dptr is NULL");
     *dptr = nullptr;
     if (bytes == 0) return;
-    ENQ_HIP(hipMalloc(dptr, bytes));
+    const size_t c = size_class(bytes);
+    std::lock_guard<std::mutex> lock(g_blocks.mu);
+    auto it = g_blocks.idle.find(c);
+    void* p = nullptr;
+    if (it != g_blocks.idle.end() && !it->second.empty()) {
+      p = it->second.back();
+      it->second.pop_back();
+    } else if (hipMalloc(&p, c) != hipSuccess) {
+      (void)hipGetLastError();
+      release_idle_locked();  // give the cached blocks back and try once more
+      ENQ_HIP(hipMalloc(&p, c));
+    }
+    g_blocks.live[p] = c;
+    *dptr = p;
   });
 }
 
@@ -187,9 +241,20 @@ int enq_free(void* dptr) {
   return guarded([&] {
     require_init();
     if (dptr == nullptr) return;
-    // Work already enqueued may still use the buffer.
-    ENQ_HIP(hipStreamSynchronize(stream()));
-    ENQ_HIP(hipFree(dptr));
+    std::lock_guard<std::mutex> lock(g_blocks.mu);
+    auto it = g_blocks.live.find(dptr);
+    ENQ_REQUIRE(it != g_blocks.live.end(), "enq_free: %p was not allocated by enq_malloc",
+                dptr);
+    g_blocks.idle[it->second].push_back(dptr);
+    g_blocks.live.erase(it);
+  });
+}
+
+int enq_release_cached_memory(void) {
+  return guarded([&] {
+    require_init();
+    std::lock_guard<std::mutex> lock(g_blocks.mu);
+    release_idle_locked();
   });
 }
 

@@ -72,13 +72,22 @@ class _KV:
 class KVCache:
     """Per-stream decoding state (``kvcache.py:23-64``): cached K/V per
     attention layer, cached residual-save activations, and the absolute
-    position of the next token."""
+    position of the next token.
 
-    def __init__(self) -> None:
+    ``trust_weights`` (not in the reference) is a promise that the model's
+    weight and bias arrays are not modified in place during the session:
+    each step then reuses the layers' device weights, biases and attention
+    buffers instead of re-validating the int8 weights against the host
+    arrays (a full hash of every weight per step) and uploading the biases
+    again.  Arrays replaced by new objects are still picked up."""
+
+    def __init__(self, trust_weights: bool = False) -> None:
         self.kv: Dict[int, _KV] = {}
         self.residual: Dict[int, DeviceArray] = {}
         self.residual_dtype: Dict[int, Any] = {}  # host dtype the reference would hold
         self.position: int = 0
+        self.trust_weights = bool(trust_weights)
+        self._resources: Dict[Any, Any] = {}  # trusted sessions: per-layer device resources
 
     def __repr__(self) -> str:
         return f"KVCache(position={self.position}, attention_layers={sorted(self.kv)})"
@@ -105,6 +114,23 @@ class KVCache:
         self.reorder([0] * int(size))
 
 
+def _layer_ids(layer: Dict[str, Any]) -> tuple:
+    return tuple(id(v) for v in layer.values() if isinstance(v, np.ndarray))
+
+
+def _resources(cache: KVCache, key: Any, layer: Dict[str, Any], make: Any) -> Any:
+    """``make()``, or in a trusted session the result kept for ``key`` while
+    the layer's arrays are the same objects."""
+    if not cache.trust_weights:
+        return make()
+    ids = _layer_ids(layer)
+    kept = cache._resources.get(key)
+    if kept is None or kept[0] != ids:
+        kept = (ids, make())
+        cache._resources[key] = kept
+    return kept[1]
+
+
 def _attention_step(x: DeviceArray, layer: Dict[str, Any], idx: int, cache: KVCache,
                     pos: int, variant: str) -> DeviceArray:
     """kvcache.py:121-213 for the softmax, absolute-position branch."""
@@ -115,7 +141,7 @@ def _attention_step(x: DeviceArray, layer: Dict[str, Any], idx: int, cache: KVCa
             "cannot represent).")
     _check_supported(layer, False)
     B, S_new, _ = x.shape
-    plan = MhaPlan(layer, B, S_new)
+    plan = _resources(cache, ("mha", idx, B, S_new), layer, lambda: MhaPlan(layer, B, S_new))
     n_all = plan.wqkv.shape[0]
     dense_w8(x, plan.wqkv, plan.bqkv, "linear", variant=variant, out=plan.qkv)
     entry = cache.kv.get(idx)
@@ -179,9 +205,12 @@ def cached_forward_step(model: Any, inputs: Any, cache: KVCache, advance_positio
             dtype = np.result_type(dtype, np.asarray(layer["gamma"]).dtype,
                                    np.asarray(layer["beta"]).dtype)
         elif t == "dense":
-            w = int8_weights(layer, "weights")
+            def make(layer=layer):
+                w = int8_weights(layer, "weights")
+                return w, _bias(layer, "bias", w.shape[0])
+            w, b = _resources(cache, ("dense", idx), layer, make)
             dtype = np.float64 if layer["activation"] in _FLOAT64_ACTIVATIONS else np.float32
-            x = dense_w8(x, w, _bias(layer, "bias", w.shape[0]), layer["activation"],
+            x = dense_w8(x, w, b, layer["activation"],
                          layer.get("activation_params", {}), variant,
                          act_quant=layer.get("act_quant"), out_dtype=dtype)
         elif t == "dropout":

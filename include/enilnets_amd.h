@@ -100,8 +100,15 @@ int enq_get_stream(void** stream);
 int enq_set_stream(void* stream);
 
 /* ---- device memory -------------------------------------------------- */
+/* Device buffers from a caching allocator: enq_free keeps the block for the
+ * next enq_malloc of its size class instead of returning it to HIP (work
+ * already enqueued on the library stream may still use it; later work on
+ * the same stream is ordered after it).  No counterpart in the reference,
+ * which holds NumPy arrays on the host. */
 int enq_malloc(void** dptr, size_t bytes);
 int enq_free(void* dptr);
+/* Synchronises the stream and returns every cached idle block to HIP. */
+int enq_release_cached_memory(void);
 int enq_copy_to_device(void* dst, const void* host_src, size_t bytes);
 int enq_copy_to_host(void* host_dst, const void* src, size_t bytes);
 int enq_copy_on_device(void* dst, const void* src, size_t bytes);

@@ -113,3 +113,32 @@ def test_beam_reorder_gathers_rows(gpu):
     cache.reorder([2, 2, 0])
     after = cached_forward_step(m, np.array([[1], [1], [1]]), cache)
     assert np.allclose(after[0], after[1], rtol=0, atol=0)
+
+
+def test_trusted_weights_session(gpu):
+    # a session that promises unchanged weights gives the same steps, and a
+    # weight replaced by a new array is still picked up
+    rng = np.random.default_rng(11)
+    m = decoder(rng)
+    tokens = rng.integers(0, 50, (2, 12))
+    plain, _ = step_all(m, tokens, prime=5)
+    cache = KVCache(trust_weights=True)
+    outs = [cached_forward_step(m, tokens[:, :5], cache)]
+    for t in range(5, 12):
+        outs.append(cached_forward_step(m, tokens[:, t:t + 1], cache))
+    trusted = np.concatenate(outs, axis=1)
+    assert np.array_equal(trusted, plain)
+    # replace the output layer's weights (a new array) in the middle of a
+    # trusted session: the next step uses them.  That layer follows every
+    # attention layer, so a fresh session over the changed model holds the
+    # same K/V history.
+    t_cache = KVCache(trust_weights=True)
+    cached_forward_step(m, tokens[:, :5], t_cache)
+    last = m.layers[-1]
+    last["weights"] = last["weights"] * np.float32(0.5)
+    ea.quantize_weights(m, per_channel=True)
+    got = cached_forward_step(m, tokens[:, 5:6], t_cache)
+    fresh = KVCache()
+    cached_forward_step(m, tokens[:, :5], fresh)
+    want = cached_forward_step(m, tokens[:, 5:6], fresh)
+    assert np.array_equal(got, want)
