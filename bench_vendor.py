@@ -52,6 +52,17 @@ def main():
     tf = 2.0 * 4096 * 8192 * 8192 / ms / 1e9
     out["bf16_linear_4096x8192x8192"] = {"ms": ms, "TFLOP/s": tf,
                                          "frac_bf16_peak": tf / BF16_PEAK_TFLOPS}
+    del a, w
+    # the MLP layer shapes of the headline (batch 4096), bf16 and fp32
+    for dt in (torch.bfloat16, torch.float32):
+        for n, k in ((1024, 784), (1024, 1024)):
+            a = torch.randn(4096, k, dtype=dt, device="cuda", generator=g)
+            w = torch.randn(n, k, dtype=dt, device="cuda", generator=g)
+            b = torch.randn(n, dtype=dt, device="cuda", generator=g)
+            ms = time_ms(lambda: torch.nn.functional.linear(a, w, b), reps=50)
+            tf = 2.0 * 4096 * n * k / ms / 1e9
+            name = "bf16" if dt == torch.bfloat16 else "fp32"
+            out[f"{name}_linear_4096x{n}x{k}"] = {"ms": ms, "TFLOP/s": tf}
     print(json.dumps({"library": f"torch {torch.__version__} (hipBLASLt)", "results": out}))
 
 

@@ -282,21 +282,24 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
   // passed the barrier.  `issued` is the last stage issued so far.
   auto wait_stage = [&](int t, int issued) {
     const int later = (issued < ktiles - 1 ? issued : ktiles - 1) - t;
-    wait_stages_after<DMA_PER_WAVE, STAGES - 2>(later);
+    wait_stages_after<DMA_PER_WAVE, STAGES - 1>(later);
   };
 
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
+  for (int s = 0; s < STAGES; ++s)
     if (s < ktiles) issue(s);
-  wait_stage(0, STAGES - 2);
+  wait_stage(0, STAGES - 1);
   wait_lgkmcnt0();  // no scalar loads pending: the loop's partial LDS waits stay exact
   block_barrier();
   read_frags(0, 0);
 
   // Software pipeline per stage t:
   //   read k-step 1 of t | MFMA k-step 0 of t | wait stage t+1, barrier,
-  //   DMA stage t+3 | read k-step 0 of t+1 | MFMA k-step 1 of t
-  // MFMAs stay in flight across the barrier and every LDS read overlaps MFMAs.
+  //   DMA stage t+STAGES into the slot of t | read k-step 0 of t+1 |
+  //   MFMA k-step 1 of t
+  // Past the barrier no wave reads stage t again, so its slot is refilled at
+  // once and all STAGES slots stay in flight.  MFMAs stay in flight across
+  // the barrier and every LDS read overlaps MFMAs.
   for (int t = 0; t < ktiles; ++t) {
     read_frags(t, 1);
     wait_lgkmcnt<FM + FN>();  // k-step 0 fragments landed, k-step 1 in flight
@@ -305,9 +308,9 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
     sched_fence();
     wait_lgkmcnt0();
     if (t + 1 < ktiles) {
-      wait_stage(t + 1, t + STAGES - 2);
+      wait_stage(t + 1, t + STAGES - 1);
       block_barrier();
-      if (t + STAGES - 1 < ktiles) issue(t + STAGES - 1);
+      if (t + STAGES < ktiles) issue(t + STAGES);
       read_frags(t + 1, 0);
     }
     sched_fence();

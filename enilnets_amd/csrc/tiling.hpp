@@ -92,6 +92,12 @@ __device__ __forceinline__ void wait_lgkmcnt() {
 // Keeps the machine scheduler from moving any instruction across this point.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// Keeps every memory access on its side of this point, in the IR passes and
+// the machine scheduler alike (sched_fence alone does not stop IR passes from
+// sinking loads towards their first use).  Placed after a block of LDS reads,
+// it makes all of them issue before the arithmetic that consumes them.
+__device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
+
 // Workgroup barrier that neither waits for outstanding loads nor lets the
 // compiler move memory operations across it.
 __device__ __forceinline__ void block_barrier() {
