@@ -887,11 +887,16 @@ void w8_ring_kernel(
   // read stage t's fragments and stage t + 1's raw tile, run stage t's
   // MFMAs, and expand stage t + 1 into the other bf16 buffer while they
   // execute.
-  for (int t = 0; t < ktiles; ++t) {
-    if (t + 1 < ktiles) wait_stage(t + 1, t + AHEAD - 1);
+  // The steady part (stage t + AHEAD exists) has a fixed wait count and no
+  // branch; the last AHEAD stages drain the ring.
+  auto stage = [&](int t, auto steady) {
+    if constexpr (decltype(steady)::value)
+      wait_vmcnt<(AHEAD - 2) * DPW>();  // stages t+2 .. t+AHEAD-1 may fly
+    else if (t + 1 < ktiles)
+      wait_stage(t + 1, t + AHEAD - 1);
     wait_lgkmcnt0();  // this wave's expansion writes of stage t are done
     block_barrier();
-    if (t + AHEAD < ktiles) issue(t + AHEAD);
+    if constexpr (decltype(steady)::value) issue(t + AHEAD);
     // every LDS read of the iteration issues before the first MFMA (stage
     // t's fragments, then stage t + 1's raw tile, whose conversion then
     // issues among the MFMAs); the last iteration expands a stage past the
@@ -910,7 +915,10 @@ void w8_ring_kernel(
             acc[i][j] = mfma_32x32x16_bf16(fa[p][i][ks], fb[j][ks], acc[i][j]);
     convert_store(t + 1);
     sched_fence();
-  }
+  };
+  int t = 0;
+  for (; t + AHEAD < ktiles; ++t) stage(t, std::true_type{});
+  for (; t < ktiles; ++t) stage(t, std::false_type{});
 
   const int lhalf = lane >> 5;
   with_activation<(C::BM <= 128)>(ep, [&](auto act) {

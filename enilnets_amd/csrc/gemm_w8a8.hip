@@ -300,23 +300,32 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
   // Past the barrier no wave reads stage t again, so its slot is refilled at
   // once and all STAGES slots stay in flight.  MFMAs stay in flight across
   // the barrier and every LDS read overlaps MFMAs.
-  for (int t = 0; t < ktiles; ++t) {
+  // The steady part (stage t + STAGES exists) has a fixed wait count and no
+  // branch; the last STAGES stages drain the ring.
+  auto stage = [&](int t, auto steady) {
     read_frags(t, 1);
     wait_lgkmcnt<FM + FN>();  // k-step 0 fragments landed, k-step 1 in flight
     sched_fence();
     mfmas(0);
     sched_fence();
     wait_lgkmcnt0();
-    if (t + 1 < ktiles) {
+    if constexpr (decltype(steady)::value) {
+      wait_vmcnt<(STAGES - 2) * DMA_PER_WAVE>();  // stages t+2 .. t+STAGES-1 may fly
+      block_barrier();
+      issue(t + STAGES);
+      read_frags(t + 1, 0);
+    } else if (t + 1 < ktiles) {
       wait_stage(t + 1, t + STAGES - 1);
       block_barrier();
-      if (t + STAGES < ktiles) issue(t + STAGES);
       read_frags(t + 1, 0);
     }
     sched_fence();
     mfmas(1);
     sched_fence();
-  }
+  };
+  int t = 0;
+  for (; t + STAGES < ktiles; ++t) stage(t, std::true_type{});
+  for (; t < ktiles; ++t) stage(t, std::false_type{});
 
   // epilogue: lane holds column l % 32; register e holds row
   // 8 * (e / 4) + 4 * (l / 32) + e % 4 of each 32 x 32 block.  One block row
