@@ -122,7 +122,11 @@ def test_dense_w8_rejects_bad_shapes(gpu):
 
 W8A8_SHAPES = [(1, 64, 64), (7, 100, 33), (16, 8192, 512), (64, 784, 1024), (200, 1000, 300),
                (256, 1024, 1024), (512, 4096, 1024), (1000, 48, 10), (130, 16, 70),
-               (4096, 1024, 4096)]
+               (4096, 1024, 4096),
+               # 256 x 256 ring kernel (>= 128 tiles): a single K stage, a K
+               # shorter than the ring, and a K tail with partial row and
+               # column tiles
+               (4096, 16, 2048), (4096, 208, 2048), (4000, 1040, 2100)]
 
 
 @pytest.mark.parametrize("m,k,n", W8A8_SHAPES)
