@@ -635,9 +635,12 @@ __global__ __launch_bounds__(WM * WN * 64) void w8_gemm_kernel(
 // 2 g and 2 g + 1 of an A or bf16 B row.
 // ---------------------------------------------------------------------------
 // FUSED_A: A arrives as the fp32 activations themselves (128-byte rows per
-// stage, 16-byte chunks swapped on bit 1 of the row: swz128) and each stage
-// is split into bf16 hi / lo planes once per workgroup, into a
-// double-buffered copy laid out like the split planes; no separate pass.
+// stage, 16-byte chunks XOR-swizzled by swz_a32) and each wave reads its
+// 8-float runs straight from the ring and splits them into bf16 hi / lo
+// fragments in registers; no separate pass.  Splitting once per workgroup
+// into a double-buffered LDS copy instead moves a quarter more LDS bytes per
+// stage and needs 32 KiB more LDS; it measured 1.5% slower on the MLP layer
+// (4096 x 1024 x 1024).
 template <int BM_, int BN_, int WM_, int WN_, int PLANES_, int STAGES_, bool FUSED_A_ = false>
 struct RingCfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, PLANES = PLANES_;
@@ -650,23 +653,24 @@ struct RingCfg {
   static constexpr int B_BYTES = BN * 32;            // code rows of 32 bytes
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int BCONV_BYTES = BN * 64;         // one bf16 copy of a B tile
-  static constexpr int ACONV_BYTES = FUSED_A ? PLANES * BM * 64 : 0;  // one split copy of A
   static constexpr int A_BLOCKS = A_BYTES / 1024, B_BLOCKS = B_BYTES / 1024;
   static constexpr int BLOCKS = A_BLOCKS + B_BLOCKS;
   // every wave issues the same number of 1 KiB blocks (vmcnt accounting);
   // waves past the last block repeat it, rewriting identical bytes
   static constexpr int DMA_PER_WAVE = (BLOCKS + NT / 64 - 1) / (NT / 64);
   static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole 1 KiB blocks");
-  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES + 2 * BCONV_BYTES + 2 * ACONV_BYTES;
+  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES + 2 * BCONV_BYTES;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
   static_assert((4 * BN) % NT == 0, "whole 8-code expansion items per thread");
-  static_assert(!FUSED_A || (4 * BM) % NT == 0, "whole split items per thread");
 };
 
 __device__ __forceinline__ int swz32(int row, int half) { return half ^ ((row >> 3) & 1); }
-// fp32 A rows: 16-byte chunks XOR bit 1 of the row, so the 16 lanes reading
-// chunk 2c (or 2c + 1) of four consecutive rows hit distinct banks.
-__device__ __forceinline__ int swz128(int row, int chunk) { return chunk ^ ((row >> 1) & 1); }
+// fp32 A rows of 128 bytes (8 chunks of 16): chunk XOR bits 1-3 of the row.
+// A fragment read takes the same logical chunk of 32 consecutive rows; any
+// 16 consecutive rows then cover the 16 chunk slots of two rows' 256 bytes
+// (row parity x swizzled chunk) once each, so every 16 lanes are
+// conflict-free.
+__device__ __forceinline__ int swz_a32(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 // One workgroup per CU (the ring's LDS), so NT / 256 waves per SIMD: said
 // to the compiler, which otherwise assumes eight and trades the registers
@@ -710,7 +714,7 @@ void w8_ring_kernel(
     const int blk = min(wave * DPW + j, C::BLOCKS - 1);
     if (C::FUSED_A && blk < C::A_BLOCKS) {
       const int r = blk * 8 + (lane >> 3);
-      const int chunk = swz128(r, lane & 7);                // logical chunk: 4 floats
+      const int chunk = swz_a32(r, lane & 7);               // logical chunk: 4 floats
       int64_t g = m0 + r;
       g = g < m ? g : m - 1;
       src[j] = reinterpret_cast<const char*>(x + g * k);
@@ -737,12 +741,9 @@ void w8_ring_kernel(
   }
   const int ktiles = int(kp / BK);
   const void* zero = g_zero16;
-  // Stages issued ahead of the one being multiplied.  The planes variant
-  // reads its A fragments from the ring in iteration t, so stage t's slot is
-  // refilled in iteration t + 1.  The fused variant is done with stage t's
-  // slot one iteration earlier (it only expands it), but prefetching that
-  // one stage further measured slower on the MLP layers (37.0 against
-  // 35.2 us at 4096 x 1024 x 1024), so both keep one slot back.
+  // Stages issued ahead of the one being multiplied: the A fragments of
+  // stage t are read from the ring in iteration t, so stage t's slot is
+  // refilled in iteration t + 1.
   constexpr int AHEAD = STAGES - 1;
   auto issue = [&](int t) {
     const uint32_t dst = lds_addr(lds) + (t % STAGES) * C::STAGE_BYTES;
@@ -781,11 +782,20 @@ void w8_ring_kernel(
   const int lrow = lane & 31, g = lane >> 5;
 
   // bf16 copies of the B tiles, double-buffered after the ring: each tile
-  // is expanded once per workgroup instead of once per wave that reads it;
-  // likewise the split A planes of the fused variant
+  // is expanded once per workgroup instead of once per wave that reads it
   char* bconv = lds + STAGES * C::STAGE_BYTES;
-  char* aconv = bconv + 2 * C::BCONV_BYTES;
   int a_off[PLANES][FM][2], b_off[FN][2];
+  // fused A: half h of the 8-float run of MFMA step ks, row of fragment i
+  // (k = 16 g + 8 ks + [0, 8): logical chunks 4 g + 2 ks + h)
+  int ar_off[FM][2][2];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int r = wm * TM + i * 32 + lrow;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) ar_off[i][ks][h] = r * 128 + 16 * swz_a32(r, 4 * g + 2 * ks + h);
+  }
 #pragma unroll
   for (int p = 0; p < PLANES; ++p)
 #pragma unroll
@@ -804,11 +814,8 @@ void w8_ring_kernel(
   // Expansion items, every thread the same number so that no branch splits
   // the loop body: piece q of 8 codes of B row cr (logical bytes 8 q ..
   // 8 q + 7 of the 32-code row) becomes logical 16-byte chunk q of the bf16
-  // row; fused split item a: 8 floats (logical chunks 2 ag and 2 ag + 1) of
-  // A row ar, which become chunk ag of that row in each plane.
+  // row.
   constexpr int B_ITEMS = 4 * BN / C::NT;
-  constexpr int A_ITEMS = C::FUSED_A ? 4 * BM / C::NT : 0;
-  constexpr int A_SLOTS = A_ITEMS > 0 ? A_ITEMS : 1;
   int conv_src[B_ITEMS], conv_dst[B_ITEMS];
 #pragma unroll
   for (int it = 0; it < B_ITEMS; ++it) {
@@ -816,61 +823,59 @@ void w8_ring_kernel(
     conv_src[it] = C::A_BYTES + cr * 32 + 16 * swz32(cr, q >> 1) + 8 * (q & 1);
     conv_dst[it] = cr * 64 + 16 * swz64(cr, q);
   }
-  int split_src0[A_SLOTS], split_src1[A_SLOTS], split_dst[A_SLOTS];
-#pragma unroll
-  for (int it = 0; it < A_SLOTS; ++it) {
-    const int item = tid + it * C::NT, ar = item >> 2, ag = item & 3;
-    split_src0[it] = ar * 128 + 16 * swz128(ar, 2 * ag);
-    split_src1[it] = ar * 128 + 16 * swz128(ar, 2 * ag + 1);
-    split_dst[it] = ar * 64 + 16 * swz64(ar, ag);
-  }
   // expansion of stage t in two halves: the LDS reads, issued beside the
   // fragment reads, and the conversion and LDS writes, scheduled among the
   // MFMAs so that they issue while the MFMAs execute
   uint2 craw[B_ITEMS];
-  float4 sa[A_SLOTS], sb[A_SLOTS];
   auto convert_load = [&](int t) {
     const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) craw[it] = *reinterpret_cast<const uint2*>(st + conv_src[it]);
-#pragma unroll
-    for (int it = 0; it < A_ITEMS; ++it) {
-      sa[it] = *reinterpret_cast<const float4*>(st + split_src0[it]);
-      sb[it] = *reinterpret_cast<const float4*>(st + split_src1[it]);
-    }
   };
   auto convert_store = [&](int t) {
     char* bdst = bconv + (t & 1) * C::BCONV_BYTES;
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it)
       *reinterpret_cast<bf16x8*>(bdst + conv_dst[it]) = codes8_to_bf16(craw[it].x, craw[it].y);
-    char* adst = aconv + (t & 1) * C::ACONV_BYTES;
-#pragma unroll
-    for (int it = 0; it < A_ITEMS; ++it) {
-      const float v[8] = {sa[it].x, sa[it].y, sa[it].z, sa[it].w,
-                          sb[it].x, sb[it].y, sb[it].z, sb[it].w};
-      Pack8 hi, lo;
-      split8<PLANES>(v, hi, lo);
-      *reinterpret_cast<Pack8*>(adst + split_dst[it]) = hi;
-      if (PLANES == 2) *reinterpret_cast<Pack8*>(adst + BM * 64 + split_dst[it]) = lo;
-    }
   };
   bf16x8 fa[PLANES][FM][2], fb[FN][2];
+  float4 araw[FM][2][2];  // fused A: the raw fp32 runs, split by split_frags
   auto read_frags = [&](int t) {
-    const char* st = C::FUSED_A ? aconv + (t & 1) * C::ACONV_BYTES
-                                : lds + (t % STAGES) * C::STAGE_BYTES;
+    const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
     const char* bt = bconv + (t & 1) * C::BCONV_BYTES;
     // in the order the MFMAs consume them
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-      for (int p = 0; p < PLANES; ++p)
+      for (int i = 0; i < FM; ++i) {
+        if constexpr (C::FUSED_A) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
-          fa[p][i][ks] = *reinterpret_cast<const bf16x8*>(st + a_off[p][i][ks]);
+          for (int h = 0; h < 2; ++h)
+            araw[i][ks][h] = *reinterpret_cast<const float4*>(st + ar_off[i][ks][h]);
+        } else {
+#pragma unroll
+          for (int p = 0; p < PLANES; ++p)
+            fa[p][i][ks] = *reinterpret_cast<const bf16x8*>(st + a_off[p][i][ks]);
+        }
+      }
 #pragma unroll
       for (int j = 0; j < FN; ++j)
         fb[j][ks] = *reinterpret_cast<const bf16x8*>(bt + b_off[j][ks]);
+    }
+  };
+  auto split_frags = [&]() {
+    if constexpr (C::FUSED_A) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const float4 u = araw[i][ks][0], w4 = araw[i][ks][1];
+          const float v[8] = {u.x, u.y, u.z, u.w, w4.x, w4.y, w4.z, w4.w};
+          Pack8 hi, lo;
+          split8<PLANES>(v, hi, lo);
+          fa[0][i][ks] = __builtin_bit_cast(bf16x8, hi);
+          if constexpr (PLANES == 2) fa[PLANES - 1][i][ks] = __builtin_bit_cast(bf16x8, lo);
+        }
     }
   };
 
@@ -904,6 +909,7 @@ void w8_ring_kernel(
     read_frags(t);
     convert_load(t + 1);
     issue_fence();
+    split_frags();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
