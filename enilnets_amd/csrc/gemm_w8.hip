@@ -661,6 +661,9 @@ struct RingCfg {
   static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole 1 KiB blocks");
   static constexpr int LDS_BYTES = STAGES * STAGE_BYTES + 2 * BCONV_BYTES;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  // workgroups the LDS lets a CU hold, and so the waves per SIMD
+  static constexpr int WG_PER_CU = (160 * 1024) / LDS_BYTES;
+  static constexpr int WAVES_PER_EU = (NT / 256) * WG_PER_CU < 8 ? (NT / 256) * WG_PER_CU : 8;
   static_assert((4 * BN) % NT == 0, "whole 8-code expansion items per thread");
 };
 
@@ -672,11 +675,12 @@ __device__ __forceinline__ int swz32(int row, int half) { return half ^ ((row >>
 // conflict-free.
 __device__ __forceinline__ int swz_a32(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
-// One workgroup per CU (the ring's LDS), so NT / 256 waves per SIMD: said
-// to the compiler, which otherwise assumes eight and trades the registers
-// that would hold a whole stage's fragments for occupancy it never gets.
+// The ring's LDS bounds the workgroups per CU, and so the waves per SIMD:
+// said to the compiler, which otherwise assumes eight and trades the
+// registers that would hold a whole stage's fragments for occupancy it never
+// gets.
 template <class C, bool KTAIL>
-__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT / 256, C::NT / 256)))
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WAVES_PER_EU, C::WAVES_PER_EU)))
 void w8_ring_kernel(
     const uint16_t* __restrict__ xa, int64_t plane_stride, int64_t kp,
     const float* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ scale,
@@ -1210,7 +1214,9 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
       // mid-size GEMM: the 128 x 128 kernel splits the activations itself.
       // MLP step with this kernel: 0.080 ms at 4 stages against
       // 0.083 at 5, 0.095 at 3, 0.089 for 64 x 128 tiles (two workgroups per
-      // CU) and 0.119 for 64 x 64.
+      // CU) and 0.119 for 64 x 64.  With the A split in registers, 64 x 128
+      // tiles of four waves (two workgroups per CU) again lost: 38.9 against
+      // 34.1 us for the 4096 x 1024 x 1024 layer.
       with_modes(kmode, [&](auto planes_tag, auto) {
         constexpr int P = decltype(planes_tag)::value;
         launch_w8_ring<RingCfg<128, 128, 4, 2, P, 4, true>>(nullptr, 0, kp, codes, w_scale, bias,
