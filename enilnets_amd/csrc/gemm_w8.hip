@@ -784,6 +784,18 @@ void w8_ring_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   const int lrow = lane & 31, g = lane >> 5;
+  // the epilogue's column scales and biases, loaded before the first DMA so
+  // that they arrive during the main loop (a launch with one tile per CU
+  // would otherwise wait a memory round trip after its last MFMA); being
+  // older than every DMA they only make the stage waits conservative
+  float col_scale[FN], col_bias[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    int64_t col = n0 + wn * TN + j * 32 + lrow;
+    col = col < n ? col : n - 1;
+    col_scale[j] = scale[col];
+    col_bias[j] = bias ? bias[col] : 0.f;
+  }
 
   // bf16 copies of the B tiles, double-buffered after the ring: each tile
   // is expanded once per workgroup instead of once per wave that reads it
@@ -942,8 +954,8 @@ void w8_ring_kernel(
     for (int j = 0; j < FN; ++j) {
       const int64_t col = n0 + wn * TN + j * 32 + lrow;
       if (col >= n) continue;
-      const float s = scale[col];
-      const float b = bias ? bias[col] : 0.f;
+      const float s = col_scale[j];
+      const float b = col_bias[j];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll

@@ -277,6 +277,17 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = mfma_32x32x32_i8(fa[ks][i], fb[ks][j], acc[i][j]);
   };
+  // the epilogue's column scales and biases, loaded before the first DMA so
+  // that they arrive during the main loop; being older than every DMA they
+  // only make the stage waits conservative
+  float sw[FN], bj[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    int64_t col = n0 + wn * TN + j * 32 + lrow;
+    col = col < n ? col : n - 1;
+    sw[j] = w_scale[col];
+    bj[j] = bias ? bias[col] : 0.f;
+  }
   // Stage t is complete for every wave once this wave's own DMA for it has
   // landed (vmcnt counts the later stages still in flight) and all waves
   // passed the barrier.  `issued` is the last stage issued so far.
@@ -330,14 +341,6 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
   // epilogue: lane holds column l % 32; register e holds row
   // 8 * (e / 4) + 4 * (l / 32) + e % 4 of each 32 x 32 block.  One block row
   // at a time, so only its 16 row scales are live beside the accumulators.
-  float sw[FN], bj[FN];
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    int64_t col = n0 + wn * TN + j * 32 + lrow;
-    col = col < n ? col : n - 1;
-    sw[j] = w_scale[col];
-    bj[j] = bias ? bias[col] : 0.f;
-  }
   with_activation<false>(ep, [&](auto act) {
     static_for<0, FM>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
