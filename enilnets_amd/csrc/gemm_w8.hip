@@ -749,10 +749,11 @@ void w8_ring_kernel(
   // stage t are read from the ring in iteration t, so stage t's slot is
   // refilled in iteration t + 1.
   constexpr int AHEAD = STAGES - 1;
-  auto issue = [&](int t) {
+  // blocks [J0, J1) of this wave's share of stage t
+  auto issue_blocks = [&](int t, auto j0, auto j1) {
     const uint32_t dst = lds_addr(lds) + (t % STAGES) * C::STAGE_BYTES;
 #pragma unroll
-    for (int j = 0; j < DPW; ++j) {
+    for (int j = decltype(j0)::value; j < decltype(j1)::value; ++j) {
       const int blk = min(wave * DPW + j, C::BLOCKS - 1);
       // A planes hold 2 bytes per K column, B codes 1 byte
       const void* sp;
@@ -770,6 +771,14 @@ void w8_ring_kernel(
       dma16(sp, dst + blk * 1024);
     }
   };
+  // The steady loop issues a stage's DMA in two groups, the second after the
+  // first half of the MFMAs, so the eight waves' blocks do not all reach the
+  // memory pipeline at once after the barrier (as in the W8A8 ring).
+  constexpr int DMA_HALF = DPW / 2;
+  using JA = std::integral_constant<int, 0>;
+  using JB = std::integral_constant<int, DMA_HALF>;
+  using JC = std::integral_constant<int, DPW>;
+  auto issue = [&](int t) { issue_blocks(t, JA{}, JC{}); };
   auto wait_stage = [&](int t, int issued) {
     const int later = (issued < ktiles - 1 ? issued : ktiles - 1) - t;
     wait_stages_after<DPW, AHEAD - 1>(later);
@@ -918,7 +927,7 @@ void w8_ring_kernel(
     wait_lgkmcnt0();  // this wave's expansion writes of stage t are done
     block_barrier();
     if constexpr (decltype(steady)::value)
-      issue(t + AHEAD);
+      issue_blocks(t + AHEAD, JA{}, JB{});
     else if (t + AHEAD < ktiles)
       issue(t + AHEAD);
     // every LDS read of the iteration issues before the first MFMA (stage
@@ -929,8 +938,7 @@ void w8_ring_kernel(
     convert_load(t + 1);
     issue_fence();
     split_frags();
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    auto mfma_step = [&](int ks) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -938,6 +946,14 @@ void w8_ring_kernel(
 #pragma unroll
           for (int p = 0; p < PLANES; ++p)
             acc[i][j] = mfma_32x32x16_bf16(fa[p][i][ks], fb[j][ks], acc[i][j]);
+    };
+    mfma_step(0);
+    if constexpr (decltype(steady)::value) {
+      sched_fence();
+      issue_blocks(t + AHEAD, JB{}, JC{});
+      sched_fence();
+    }
+    mfma_step(1);
     convert_store(t + 1);
     sched_fence();
   };
