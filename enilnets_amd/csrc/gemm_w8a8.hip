@@ -282,9 +282,13 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
       for (int j = 0; j < FN; ++j) acc[i][j] = mfma_32x32x32_i8(fa[ks][i], fb[ks][j], acc[i][j]);
   };
   // The steady loop issues a stage's DMA in DMA_GROUPS groups of blocks,
-  // each followed by its share of the k-step 1 MFMAs.  Same-box sweeps on
-  // 8192^3: all four blocks at once 0.636-0.651 ms, two groups 0.606-0.616,
-  // four groups 0.615-0.626.
+  // each followed by its share of the k-step 0 MFMAs: the eight waves'
+  // blocks then reach the memory pipeline spread over the MFMAs instead of
+  // all at once after the barrier (a wave stalled on a full queue cannot
+  // issue the MFMAs behind it).  Same-box sweeps on 8192^3: all blocks at
+  // once after the barrier 0.636-0.651 ms; two groups among the k-step 1
+  // MFMAs 0.606-0.616 (four groups 0.615-0.626); two groups among the
+  // k-step 0 MFMAs, one stage less ahead, 0.600-0.610.
   constexpr int DMA_GROUPS = 2;
   static_assert(DMA_PER_WAVE % DMA_GROUPS == 0 && FM * FN % DMA_GROUPS == 0, "whole shares");
   // MFMAs [Q * FM * FN / DMA_GROUPS, (Q + 1) * FM * FN / DMA_GROUPS) of
@@ -311,50 +315,47 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
   // passed the barrier.  `issued` is the last stage issued so far.
   auto wait_stage = [&](int t, int issued) {
     const int later = (issued < ktiles - 1 ? issued : ktiles - 1) - t;
-    wait_stages_after<DMA_PER_WAVE, STAGES - 1>(later);
+    wait_stages_after<DMA_PER_WAVE, STAGES - 2>(later);
   };
 
 #pragma unroll
-  for (int s = 0; s < STAGES; ++s)
+  for (int s = 0; s < STAGES - 1; ++s)
     if (s < ktiles) issue(s);
-  wait_stage(0, STAGES - 1);
+  wait_stage(0, STAGES - 2);
   wait_lgkmcnt0();  // no scalar loads pending: the loop's partial LDS waits stay exact
   block_barrier();
   read_frags(0, 0);
 
   // Software pipeline per stage t:
-  //   read k-step 1 of t | MFMA k-step 0 of t | wait stage t+1, barrier,
-  //   DMA stage t+STAGES into the slot of t | read k-step 0 of t+1 |
-  //   MFMA k-step 1 of t
-  // Past the barrier no wave reads stage t again, so its slot is refilled at
-  // once and all STAGES slots stay in flight.  MFMAs stay in flight across
-  // the barrier and every LDS read overlaps MFMAs.
-  // The steady part (stage t + STAGES exists) has a fixed wait count and no
-  // branch; the last STAGES stages drain the ring.
+  //   read k-step 1 of t | DMA stage t+STAGES-1 into the slot of t-1, in
+  //   groups among the MFMAs of k-step 0 of t | wait stage t+1, barrier |
+  //   read k-step 0 of t+1 | MFMA k-step 1 of t
+  // Every wave read stage t-1 before the previous barrier, so its slot is
+  // free.  MFMAs stay in flight across the barrier and every LDS read
+  // overlaps MFMAs.  The steady part (stage t + STAGES - 1 exists) has a
+  // fixed wait count and no branch; the last stages drain the ring.
   auto stage = [&](int t, auto steady) {
     read_frags(t, 1);
     wait_lgkmcnt<FM + FN>();  // k-step 0 fragments landed, k-step 1 in flight
     sched_fence();
-    mfmas(0);
+    if constexpr (decltype(steady)::value) {
+      static_for<0, DMA_GROUPS>([&](auto qc) {
+        constexpr int Q = decltype(qc)::value, B = DMA_PER_WAVE / DMA_GROUPS;
+        issue_blocks(t + STAGES - 1, std::integral_constant<int, Q * B>{},
+                     std::integral_constant<int, (Q + 1) * B>{});
+        sched_fence();
+        mfmas_part(0, qc);
+        sched_fence();
+      });
+    } else {
+      mfmas(0);
+    }
     sched_fence();
     wait_lgkmcnt0();
     if constexpr (decltype(steady)::value) {
       wait_vmcnt<(STAGES - 2) * DMA_PER_WAVE>();  // stages t+2 .. t+STAGES-1 may fly
       block_barrier();
-      // one DMA group before each share of the k-step 1 MFMAs: the eight
-      // waves' blocks then reach the memory pipeline spread over the MFMAs
-      // instead of all at once after the barrier (where a wave stalled on a
-      // full queue cannot issue its MFMAs)
-      static_for<0, DMA_GROUPS>([&](auto qc) {
-        constexpr int Q = decltype(qc)::value, B = DMA_PER_WAVE / DMA_GROUPS;
-        issue_blocks(t + STAGES, std::integral_constant<int, Q * B>{},
-                     std::integral_constant<int, (Q + 1) * B>{});
-        if constexpr (Q == 0) read_frags(t + 1, 0);
-        sched_fence();
-        mfmas_part(1, qc);
-        sched_fence();
-      });
-      return;
+      read_frags(t + 1, 0);
     } else if (t + 1 < ktiles) {
       wait_stage(t + 1, t + STAGES - 1);
       block_barrier();
@@ -365,7 +366,7 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
     sched_fence();
   };
   int t = 0;
-  for (; t + STAGES < ktiles; ++t) stage(t, std::true_type{});
+  for (; t + STAGES - 1 < ktiles; ++t) stage(t, std::true_type{});
   for (; t < ktiles; ++t) stage(t, std::false_type{});
 
   // epilogue: lane holds column l % 32; register e holds row
