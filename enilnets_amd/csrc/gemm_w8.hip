@@ -926,10 +926,9 @@ void w8_ring_kernel(
       wait_stage(t + 1, t + AHEAD - 1);
     wait_lgkmcnt0();  // this wave's expansion writes of stage t are done
     block_barrier();
-    if constexpr (decltype(steady)::value)
-      issue_blocks(t + AHEAD, JA{}, JB{});
-    else if (t + AHEAD < ktiles)
-      issue(t + AHEAD);
+    // the first group of the stage's DMA (the second follows k-step 0)
+    const bool refill = decltype(steady)::value || t + AHEAD < ktiles;
+    if (refill) issue_blocks(t + AHEAD, JA{}, JB{});
     // every LDS read of the iteration issues before the first MFMA (stage
     // t's fragments, then stage t + 1's raw tile, whose conversion then
     // issues among the MFMAs); the last iteration expands a stage past the
@@ -948,11 +947,9 @@ void w8_ring_kernel(
             acc[i][j] = mfma_32x32x16_bf16(fa[p][i][ks], fb[j][ks], acc[i][j]);
     };
     mfma_step(0);
-    if constexpr (decltype(steady)::value) {
-      sched_fence();
-      issue_blocks(t + AHEAD, JB{}, JC{});
-      sched_fence();
-    }
+    sched_fence();
+    if (refill) issue_blocks(t + AHEAD, JB{}, JC{});
+    sched_fence();
     mfma_step(1);
     convert_store(t + 1);
     sched_fence();
