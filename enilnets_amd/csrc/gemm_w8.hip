@@ -330,19 +330,21 @@ __global__ __launch_bounds__(512) void gemv_decode_kernel(
 }
 
 // Tall-skinny GEMV (n <= 32, any m): grid (column groups, K splits, 16-row
-// blocks).  Each wave owns a K range of `chunks` x 128 and keeps the
-// activation fragments of its rows in registers, read from fp32 and split
-// there; it then streams 16-column blocks of W (the next block's loads in
-// flight while one is multiplied), and the 8 waves' partial tiles are summed
-// through LDS.  With one K split (part == nullptr) the kernel finishes the
-// outputs itself.
-template <int PLANES, int KMODE>
+// blocks).  Each wave owns a K range of `chunks_per_wave` (<= CHUNKS) x 128
+// and keeps the activation fragments of its rows in registers, read from
+// fp32 and split there; it then streams 16-column blocks of W (the next
+// block's loads in flight while one is multiplied), and the 8 waves' partial
+// tiles are summed through LDS.  With one K split (part == nullptr) the
+// kernel finishes the outputs itself.  CHUNKS is the host's bound on
+// chunks_per_wave: loading two chunks for waves that own one (K = 1024)
+// doubled the activation requests and the registers, and the kernel streamed
+// at 2.1 TB/s.
+template <int PLANES, int KMODE, int CHUNKS>
 __global__ __launch_bounds__(512) void gemv_skinny_kernel(
     const float* __restrict__ x, int64_t m, int64_t k, int vec, const int8_t* __restrict__ w,
     int64_t n, int chunks_per_wave, int col_blocks_per_group, int64_t mp,
     float* __restrict__ part, const float* __restrict__ scale, const float* __restrict__ bias,
     Epilogue ep, float* __restrict__ y, float* __restrict__ z) {
-  constexpr int CHUNKS = 2;
   __shared__ float red[kGemvWaves][16][17];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -1140,10 +1142,12 @@ void gemv_dispatch(const GemvPlan& g, const float* x, const int8_t* w, const flo
   } else {
     // one K split: the kernel finishes the outputs itself
     const bool direct = g.splits == 1;
-    gemv_skinny_kernel<PLANES, KMODE>
-        <<<dim3(unsigned(g.groups), unsigned(g.splits), unsigned(g.m_blocks)), 512, 0,
-           stream()>>>(x, m, k, vec, w, n, g.chunks_per_wave, g.cb_per_group, g.mp,
-                       direct ? nullptr : part, scale, bias, ep, y, z);
+    ENQ_REQUIRE(g.chunks_per_wave >= 1 && g.chunks_per_wave <= 2, "skinny GEMV plan");
+    auto kernel = g.chunks_per_wave == 1 ? gemv_skinny_kernel<PLANES, KMODE, 1>
+                                         : gemv_skinny_kernel<PLANES, KMODE, 2>;
+    kernel<<<dim3(unsigned(g.groups), unsigned(g.splits), unsigned(g.m_blocks)), 512, 0,
+             stream()>>>(x, m, k, vec, w, n, g.chunks_per_wave, g.cb_per_group, g.mp,
+                         direct ? nullptr : part, scale, bias, ep, y, z);
     check_launch("gemv_skinny_kernel");
     if (direct) return;
   }
