@@ -37,6 +37,20 @@ def activation_args(name: str, params: Optional[Dict[str, Any]] = None) -> Tuple
     return _lib.ACTIVATIONS[name], float(alpha), float(clip)
 
 
+def _promotion_key(v: Any) -> Tuple[Any, ...]:
+    """What NumPy's promotion of ``v`` depends on: arrays and NumPy scalars by
+    dtype, Python scalars (weak) by type."""
+    if isinstance(v, (np.ndarray, np.generic)):
+        return (isinstance(v, np.ndarray), v.dtype.str)
+    return (type(v),)
+
+
+# result dtype of ``x / scale + zero_point`` by promotion keys and the
+# output dtype: the spec is applied per layer call, and resolving it on
+# probe values each time cost more host time than the device pass
+_AQ_RESULT: Dict[Tuple[Any, ...], Any] = {}
+
+
 def act_quant_args(spec: Dict[str, Any], out_dtype: Any = np.float32) -> Tuple[Any, ...]:
     """``(mode, scale, zero_point, qmin, qmax, result_dtype)`` of an
     ``act_quant`` spec (``forward.py:798-805``) applied to a layer output of
@@ -48,7 +62,11 @@ def act_quant_args(spec: Dict[str, Any], out_dtype: Any = np.float32) -> Tuple[A
     scale, zp = spec["scale"], spec["zero_point"]
     if np.size(scale) != 1 or np.size(zp) != 1:
         raise NotImplementedError("act_quant specs are per tensor on the quantized path")
-    res = (np.ones(1, dtype=out_dtype) / _probe(scale) + _probe(zp)).dtype
+    key = (_promotion_key(scale), _promotion_key(zp), np.dtype(out_dtype).str)
+    res = _AQ_RESULT.get(key)
+    if res is None:
+        res = (np.ones(1, dtype=out_dtype) / _probe(scale) + _probe(zp)).dtype
+        _AQ_RESULT[key] = res
     if res not in (np.float32, np.float64):
         raise NotImplementedError(f"act_quant arithmetic in {res} is not supported")
     mode = _lib.AQ_F64 if res == np.float64 else _lib.AQ_F32
