@@ -91,7 +91,18 @@ template <bool FUSE_AQ, class Body>
 __device__ __forceinline__ void with_activation(const Epilogue& ep, Body&& body) {
   if constexpr (FUSE_AQ) {
     if (ep.aq != ENQ_AQ_NONE) {
-      body([ep](float x) { return epilogue_out(x, ep); });
+      // the common activations straight-line here too, not a switch per element
+      switch (ep.activation) {
+        case ENQ_ACT_LINEAR:
+          body([ep](float x) { return fake_quant(x, ep); });
+          break;
+        case ENQ_ACT_RELU:
+          body([ep](float x) { return fake_quant(x < 0.0f ? 0.0f : x, ep); });
+          break;
+        default:
+          body([ep](float x) { return epilogue_out(x, ep); });
+          break;
+      }
       return;
     }
   }

@@ -52,6 +52,34 @@ def test_standalone_pass_bit_exact(gpu, dtype, scheme, bits):
     assert np.array_equal(got[~nan].view(np.uint32), w32[~nan].view(np.uint32))
 
 
+@pytest.mark.parametrize("scale", [0.1, 0.02, 1.0 / 3.0, 0.0234375, 3.7, 1e-3])
+@pytest.mark.parametrize("zp", [0.0, 3.0, 117.0])
+def test_standalone_pass_rounding_ties(gpu, scale, zp):
+    """Quotients x / scale + zp on and next to half-integers.  With the scale
+    rounded to 15 significant bits every (k + 0.5 - zp) * scale is a float32,
+    so those quotients are exact ties (rounded half to even); their float32
+    neighbours sit just off the tie.  The float64 path multiplies by the
+    reciprocal and must hand exact ties to the true division."""
+    e = np.floor(np.log2(scale))
+    s15 = float(np.round(scale / 2.0 ** (e - 14)) * 2.0 ** (e - 14))
+    k = np.arange(-140, 141, dtype=np.float64)
+    ties = ((k + 0.5 - zp) * s15).astype(np.float32)
+    assert np.array_equal(ties.astype(np.float64) / s15 + zp, k + 0.5)
+    up1 = np.nextafter(ties, np.float32(np.inf))
+    dn1 = np.nextafter(ties, np.float32(-np.inf))
+    up2 = np.nextafter(up1, np.float32(np.inf))
+    rng = np.random.default_rng(int(scale * 1e4) + int(zp))
+    noise = (rng.standard_normal(4096) * 140 * s15).astype(np.float32)
+    x = np.concatenate([ties, up1, dn1, up2, noise])
+    spec = {"bits": 8, "scheme": "asymmetric", "scale": np.float64(s15),
+            "zero_point": np.float64(zp)}
+    want = oracle.fake_quantize(x, spec["scale"], spec["zero_point"], 8, "asymmetric")
+    assert want.dtype == np.float64
+    got = D.act_quant(DeviceArray.from_numpy(x), spec).numpy()
+    w32 = want.astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), w32.view(np.uint32))
+
+
 def make_w(rng, n, k):
     w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
     fq, scale, _ = oracle.quantize_tensor(w, 8, per_channel=True)
