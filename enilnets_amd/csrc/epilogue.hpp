@@ -35,6 +35,13 @@ __device__ __forceinline__ float fake_quant(float v, const Epilogue& e) {
   return __fmul_rn(c - zp, s);
 }
 
+// activations.py GELU (tanh form), one element.
+__device__ __forceinline__ float gelu(float x) {
+  const float c = 0.7978845608028654f;  // sqrt(2 / pi)
+  float inner = c * (x + 0.044715f * (x * x * x));
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
 // activations.py:21-41, one element.  relu keeps -0.0 and NaN as np.maximum
 // does; softmax is a row operation and is applied by a separate kernel.
 __device__ __forceinline__ float activate(float x, const Epilogue& e) {
@@ -50,11 +57,8 @@ __device__ __forceinline__ float activate(float x, const Epilogue& e) {
       const float alp = 1.6732632423543772848170429916717f;
       return lam * (x > 0.0f ? x : alp * (expf(x) - 1.0f));
     }
-    case ENQ_ACT_GELU: {
-      const float c = 0.7978845608028654f;  // sqrt(2 / pi)
-      float inner = c * (x + 0.044715f * (x * x * x));
-      return 0.5f * x * (1.0f + tanhf(inner));
-    }
+    case ENQ_ACT_GELU:
+      return gelu(x);
     case ENQ_ACT_SWISH:
       return x * 1.0f / (1.0f + expf(-x));
     case ENQ_ACT_MISH:
@@ -113,6 +117,9 @@ __device__ __forceinline__ void with_activation(const Epilogue& ep, Body&& body)
       break;
     case ENQ_ACT_RELU:
       body([](float x) { return x < 0.0f ? 0.0f : x; });
+      break;
+    case ENQ_ACT_GELU:
+      body([](float x) { return gelu(x); });
       break;
     default:
       body([ep](float x) { return activate(x, ep); });
