@@ -78,16 +78,15 @@ __device__ __forceinline__ float activate(float x, const Epilogue& e) {
   }
 }
 
-// Calls body(f) with f the activation as a callable, so the common
-// activations compile into straight-line epilogues instead of a switch per
-// element.
 // activate, then the fake-quantization when the epilogue has one.
 __device__ __forceinline__ float epilogue_out(float x, const Epilogue& e) {
   const float a = activate(x, e);
   return e.aq != ENQ_AQ_NONE ? fake_quant(a, e) : a;
 }
 
-// FUSE_AQ instantiates the fake-quantizing variant too.  Kernels without
+// Calls body(f) with f the activation as a callable, so the common
+// activations compile into straight-line epilogues instead of a switch per
+// element.  FUSE_AQ instantiates the fake-quantizing variant too.  Kernels without
 // register headroom (the 256 x 256 tiles) leave it out: its float64
 // arithmetic next to live accumulators spills them, so their callers run the
 // fake-quantization as a separate pass (gemm_epilogue / finish_rows).
