@@ -259,3 +259,29 @@ def test_quantize_weights_keeps_device_int8_codes(gpu, shape, per_channel):
     rows = np.broadcast_to(np.asarray(want_scale, np.float32).reshape(-1), (shape[0],)) \
         if per_channel else np.full(shape[0], np.float32(want_scale))
     assert np.array_equal(wq.scale.numpy(), rows)
+
+
+@pytest.mark.parametrize("offset", [1, 2, 3])
+def test_codes_at_unaligned_offsets(gpu, offset):
+    # int8 codes written at any byte offset: the vector kernels store four
+    # codes as one 32-bit word, so they may only take a 4-byte aligned output
+    import ctypes
+    from enilnets_amd import _lib
+    rng = np.random.default_rng(offset)
+    n = 4099 * 3
+    w = (rng.standard_normal(n) * 0.05).astype(np.float32)
+    want_codes, want_scale = oracle.int8_codes(w, per_channel=False)
+    d_w = DeviceArray.from_numpy(w)
+    scale, zp = DeviceArray((1,), np.float32), DeviceArray((1,), np.float32)
+    for entry in ("enq_quantize_tensor", "enq_quantize_codes_i8"):
+        buf = DeviceArray.from_numpy(np.zeros(n + 8, np.int8))
+        dst = ctypes.c_void_p(buf.address + offset)
+        if entry == "enq_quantize_tensor":
+            _lib.call(entry, _lib.F32, d_w.ptr, 1, 1, n, 8, _lib.SYMMETRIC, None, dst,
+                      scale.ptr, zp.ptr, None)
+            same_bits(scale.numpy(), np.asarray(want_scale, np.float32).reshape(-1))
+        else:
+            _lib.call(entry, _lib.F32, d_w.ptr, 1, 1, n, scale.ptr, zp.ptr, -127, 127, dst)
+        got = buf.numpy()
+        assert np.array_equal(got[offset:offset + n], want_codes.reshape(-1)), entry
+        assert not got[:offset].any() and not got[offset + n:].any(), entry
