@@ -681,13 +681,16 @@ __device__ __forceinline__ int swz_a32(int row, int chunk) { return chunk ^ ((ro
 // said to the compiler, which otherwise assumes eight and trades the
 // registers that would hold a whole stage's fragments for occupancy it never
 // gets.
-template <class C, bool KTAIL>
+// YP: the output goes to bf16 planes (yp) instead of fp32 (y); a separate
+// instantiation, so the fp32-output kernels carry none of its registers.
+template <class C, bool KTAIL, bool YP = false>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WAVES_PER_EU, C::WAVES_PER_EU)))
 void w8_ring_kernel(
     const uint16_t* __restrict__ xa, int64_t plane_stride, int64_t kp,
     const float* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ scale,
     const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n,
-    RowGroups grp, Epilogue ep, float* __restrict__ y, float* __restrict__ z) {
+    RowGroups grp, Epilogue ep, float* __restrict__ y, float* __restrict__ z,
+    uint16_t* __restrict__ yp, int64_t yp_plane_stride, int64_t yp_ld) {
   constexpr int BM = C::BM, BN = C::BN, WN = C::WN, PLANES = C::PLANES, STAGES = C::STAGES;
   constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, BK = C::BK;
   constexpr int DPW = C::DMA_PER_WAVE;
@@ -980,7 +983,16 @@ void w8_ring_kernel(
             float v = acc[i][j][e] * s;
             if (bias) v = v + b;
             if (z) z[row * n + col] = v;
-            y[row * n + col] = act(v);
+            if constexpr (YP) {
+              // the output as the next GEMM's bf16 planes (split_planes_kernel's split)
+              const float h = act(v);
+              const uint16_t hi = bf16_bits_rne(h);
+              yp[row * yp_ld + col] = hi;
+              if constexpr (PLANES == 2)
+                yp[yp_plane_stride + row * yp_ld + col] = bf16_bits_rne(h - bf16_to_float(hi));
+            } else {
+              y[row * n + col] = act(v);
+            }
           }
         }
     }
@@ -991,7 +1003,8 @@ template <class C>
 void launch_w8_ring(const uint16_t* xa, int64_t plane_stride, int64_t kp, const int8_t* w,
                     const float* scale, const float* bias, int64_t m, int64_t n, int64_t k,
                     const Epilogue& ep, float* y, float* z, const RowGroups& grp,
-                    const float* x = nullptr) {
+                    const float* x = nullptr, uint16_t* yp = nullptr, int64_t yp_plane_stride = 0,
+                    int64_t yp_ld = 0) {
   // grouped rows: every group may end in a partial tile
   const int64_t tiles_m = ceil_div(m, C::BM) + (grp.offsets ? grp.groups : 0);
   const int64_t tiles_n = ceil_div(n, C::BN);
@@ -1003,11 +1016,23 @@ void launch_w8_ring(const uint16_t* xa, int64_t plane_stride, int64_t kp, const 
                                 hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
     ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8_ring_kernel<C, true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
+    if constexpr (!C::FUSED_A) {
+      ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8_ring_kernel<C, false, true>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
+      ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8_ring_kernel<C, true, true>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
+    }
     attr_set = true;
   }
   auto kernel = (k % C::BK == 0) ? w8_ring_kernel<C, false> : w8_ring_kernel<C, true>;
+  if constexpr (!C::FUSED_A) {
+    if (yp) kernel = (k % C::BK == 0) ? w8_ring_kernel<C, false, true> : w8_ring_kernel<C, true, true>;
+  } else {
+    ENQ_REQUIRE(yp == nullptr, "plane outputs take pre-split activations");
+  }
   kernel<<<unsigned(tiles_m * tiles_n), C::NT, lds_bytes, stream()>>>(
-      xa, plane_stride, kp, x, w, scale, bias, m, n, k, int(tiles_m), int(tiles_n), grp, ep, y, z);
+      xa, plane_stride, kp, x, w, scale, bias, m, n, k, int(tiles_m), int(tiles_n), grp, ep, y, z,
+      yp, yp_plane_stride, yp_ld);
   check_launch("w8_ring_kernel");
 }
 
@@ -1038,20 +1063,24 @@ template <int PLANES, int KMODE>
 void gemm_dispatch(const uint16_t* xa, int64_t plane_stride, int64_t kp, const int8_t* w,
                    int64_t ldw, const float* scale, const float* bias, int64_t m, int64_t n,
                    int64_t k, const Epilogue& ep, float* y, float* z,
-                   const RowGroups& grp = RowGroups{}) {
+                   const RowGroups& grp = RowGroups{}, uint16_t* yp = nullptr,
+                   int64_t yp_plane_stride = 0, int64_t yp_ld = 0) {
   const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256);
   const bool big = big_tiles >= device_cu_count();
   if (KMODE != 2) {
     if (big)
       launch_w8_ring<RingCfg<256, 256, 4, 2, PLANES, PLANES == 2 ? 3 : 4>>(
-          xa, plane_stride, kp, w, scale, bias, m, n, k, ep, y, z, grp);
+          xa, plane_stride, kp, w, scale, bias, m, n, k, ep, y, z, grp, nullptr, yp,
+          yp_plane_stride, yp_ld);
     else
       launch_w8_ring<RingCfg<128, 128, 4, 2, PLANES, 4>>(
-          xa, plane_stride, kp, w, scale, bias, m, n, k, ep, y, z, grp);
+          xa, plane_stride, kp, w, scale, bias, m, n, k, ep, y, z, grp, nullptr, yp,
+          yp_plane_stride, yp_ld);
     return;
   }
   // register-staged kernel: any K, any code alignment; no row groups
   ENQ_REQUIRE(grp.offsets == nullptr, "grouped rows need K a multiple of 16");
+  ENQ_REQUIRE(yp == nullptr, "plane outputs need K a multiple of 16");
   if (big)
     launch_gemm<256, 256, 4, 2, PLANES, KMODE>(xa, plane_stride, kp, w, ldw, scale, bias, m, n, k,
                                                ep, y, z);
@@ -1180,15 +1209,18 @@ bool grouped_gemm_supported(int64_t k, const int8_t* codes) {
 
 void dense_w8_grouped(const uint16_t* xa, int64_t plane_stride, int64_t kp, int planes,
                       int64_t m, int64_t k, const int8_t* codes, const float* w_scale, int64_t n,
-                      const float* bias, const RowGroups& grp, const Epilogue& ep, float* y) {
+                      const float* bias, const RowGroups& grp, const Epilogue& ep, float* y,
+                      uint16_t* yp, int64_t yp_plane_stride) {
   ENQ_REQUIRE(grouped_gemm_supported(k, codes), "grouped rows need K a multiple of 16");
   ENQ_REQUIRE(ep.activation != ENQ_ACT_SOFTMAX, "softmax epilogue is not fused");
+  // plane outputs have no padding columns to clear: rows of n = gemm_k_pad(n)
+  ENQ_REQUIRE(yp == nullptr || gemm_k_pad(n) == n, "plane outputs need N a multiple of 32");
   const int kmode = k % 32 == 0 ? 0 : 1;
   auto run = [&](auto planes_tag, auto kmode_tag) {
     constexpr int P = decltype(planes_tag)::value;
     constexpr int KM = decltype(kmode_tag)::value;
     gemm_dispatch<P, KM>(xa, plane_stride, kp, codes, k, w_scale, bias, m, n, k, ep, y, nullptr,
-                         grp);
+                         grp, yp, yp_plane_stride, n);
   };
   using P1 = std::integral_constant<int, 1>;
   using P2 = std::integral_constant<int, 2>;

@@ -342,9 +342,16 @@ void moe_w8(const MoeArgs& a) {
       RowGroups g1{offsets, E, a.hidden * a.d, a.hidden};
       RowGroups g2{offsets, E, a.d * a.hidden, a.d};
       split_planes(a.x, row_token, entries, a.d, planes1, entries, kp1, planes);
-      dense_w8_grouped(planes1, entries * kp1, kp1, planes, entries, a.d, a.w1, a.s1, a.hidden,
-                       a.b1, g1, a.ep, h);
-      split_planes(h, nullptr, entries, a.hidden, planes2, entries, kp2, planes);
+      if (kp2 == a.hidden) {
+        // the first GEMM writes the hidden activations straight into the
+        // second's planes (no fp32 round trip through HBM)
+        dense_w8_grouped(planes1, entries * kp1, kp1, planes, entries, a.d, a.w1, a.s1,
+                         a.hidden, a.b1, g1, a.ep, nullptr, planes2, entries * kp2);
+      } else {
+        dense_w8_grouped(planes1, entries * kp1, kp1, planes, entries, a.d, a.w1, a.s1,
+                         a.hidden, a.b1, g1, a.ep, h);
+        split_planes(h, nullptr, entries, a.hidden, planes2, entries, kp2, planes);
+      }
       dense_w8_grouped(planes2, entries * kp2, kp2, planes, entries, a.hidden, a.w2, a.s2, a.d,
                        a.b2, g2, lin, yg);
     } else {

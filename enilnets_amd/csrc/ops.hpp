@@ -27,9 +27,13 @@ int64_t gemm_k_pad(int64_t k);
 bool grouped_gemm_supported(int64_t k, const int8_t* codes);
 
 // GEMM over pre-split planes with rows in groups (`grp`), group g using
-// codes + g * grp.w_stride and w_scale / bias + g * grp.v_stride.
+// codes + g * grp.w_stride and w_scale / bias + g * grp.v_stride.  With `yp`
+// the (m, n) output is written as bf16 planes of the same split and layout
+// (plane p at yp + p * yp_plane_stride, rows of n; n a multiple of 32),
+// ready for the next grouped GEMM, instead of as fp32 into y.
 void dense_w8_grouped(const uint16_t* xa, int64_t plane_stride, int64_t kp, int planes,
                       int64_t m, int64_t k, const int8_t* codes, const float* w_scale, int64_t n,
-                      const float* bias, const RowGroups& grp, const Epilogue& ep, float* y);
+                      const float* bias, const RowGroups& grp, const Epilogue& ep, float* y,
+                      uint16_t* yp = nullptr, int64_t yp_plane_stride = 0);
 
 }  // namespace enq

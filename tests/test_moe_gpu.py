@@ -153,6 +153,25 @@ def test_moe_empty_experts(gpu):
     assert np.all(row_rel_err(out.numpy(), want) <= 1e-4)
 
 
+@pytest.mark.parametrize("d,hidden", [(64, 256), (48, 80)])
+def test_moe_layer_bf16(gpu, d, hidden):
+    # the bf16 variant (one plane per activation); hidden 256 has the first
+    # GEMM write the second's plane itself, hidden 80 (padded to 96) splits
+    # it in a separate pass.  Router logits are given, so the routing is the
+    # oracle's; rows within the bf16 Dense bound.
+    print(f"[case] moe bf16 d={d} hidden={hidden}", flush=True)
+    rng = np.random.default_rng(d + hidden)
+    m = moe_model(rng, d, hidden, 8, 2)
+    logits = rng.standard_normal((700, 8)).astype(np.float32)
+    x = rng.standard_normal((700, d)).astype(np.float32)
+    out, _ = moe_forward(DeviceArray.from_numpy(x), m.layers[0], variant="bf16",
+                         router_logits=DeviceArray.from_numpy(logits))
+    probs = softmax32(logits)
+    want = oracle.moe_forward(x.astype(np.float64), m.layers[0], probs=probs.astype(np.float64))
+    err = row_rel_err(out.numpy(), want)
+    assert np.all(err <= 2e-2), f"max row error {err.max():.3e}"
+
+
 @pytest.mark.parametrize("top_k", [1, 2, 4])
 def test_dense_mixture_invariant(gpu, top_k):
     # test_enilnets.py:8331-8353: every expert on every token densely, gated
