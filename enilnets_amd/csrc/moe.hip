@@ -69,6 +69,63 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
   }
 }
 
+// The same routing with the token's logits and probabilities held in
+// registers, for experts <= EMAX: the kernel above reads each probability
+// back from global memory after storing it, and its dynamically indexed
+// mask lives in private memory.  Same operations in the same order, so the
+// same bits.
+template <int EMAX>
+__global__ __launch_bounds__(256) void moe_route_regs_kernel(const float* __restrict__ logits,
+                                                             int64_t tokens, int experts,
+                                                             int top_k,
+                                                             float* __restrict__ probs,
+                                                             int* __restrict__ chosen,
+                                                             float* __restrict__ gates) {
+  static_assert(EMAX <= 32, "the mask is one 32-bit word");
+  const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= tokens) return;
+  const float* l = logits + t * experts;
+  float v[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) v[e] = l[e < experts ? e : 0];  // in-bounds, masked below
+  float mx = v[0];
+#pragma unroll
+  for (int e = 1; e < EMAX; ++e)
+    if (e < experts) mx = (v[e] > mx || v[e] != v[e]) ? v[e] : mx;  // np.max propagates NaN
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    if (e < experts) {
+      v[e] = expf(v[e] - mx);
+      sum = sum + v[e];
+    }
+  }
+  float* p = probs + t * experts;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    if (e < experts) {
+      v[e] = v[e] / sum;
+      p[e] = v[e];
+    }
+  }
+  uint32_t taken = 0;
+  for (int s = 0; s < top_k; ++s) {
+    int best = -1;  // top_k <= experts: an expert is always left
+    float bv = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      if (e >= experts || ((taken >> e) & 1u)) continue;
+      if (best < 0 || v[e] > bv) {
+        best = e;
+        bv = v[e];
+      }
+    }
+    taken |= 1u << best;
+    chosen[t * top_k + s] = best;
+    gates[t * top_k + s] = bv;
+  }
+}
+
 // Per-block count of the (token, slot) entries routed to each expert.
 __global__ __launch_bounds__(kSortBlock) void moe_count_kernel(const int* __restrict__ chosen,
                                                                int64_t entries, int experts,
@@ -87,16 +144,19 @@ __global__ __launch_bounds__(kSortBlock) void moe_count_kernel(const int* __rest
 // expert, and writes the group offsets (experts + 1 values).
 __global__ __launch_bounds__(256) void moe_scan_kernel(int* __restrict__ hist, int blocks,
                                                        int experts, int* __restrict__ offsets) {
+  // one wave per expert column of hist, 64 blocks at a time
   __shared__ int total[kMaxExperts];
   __shared__ int first[kMaxExperts];
-  for (int e = threadIdx.x; e < experts; e += 256) {
-    int run = 0;
-    for (int b = 0; b < blocks; ++b) {
-      const int c = hist[int64_t(b) * experts + e];
-      hist[int64_t(b) * experts + e] = run;
-      run += c;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int e = wave; e < experts; e += 4) {
+    int sum = 0;
+    for (int b0 = 0; b0 < blocks; b0 += 64) {
+      const int b = b0 + lane;
+      sum += b < blocks ? hist[int64_t(b) * experts + e] : 0;
     }
-    total[e] = run;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
+    if (lane == 0) total[e] = sum;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -109,8 +169,22 @@ __global__ __launch_bounds__(256) void moe_scan_kernel(int* __restrict__ hist, i
     offsets[experts] = run;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < experts; e += 256)
-    for (int b = 0; b < blocks; ++b) hist[int64_t(b) * experts + e] += first[e];
+  // exclusive prefix over the blocks, from the expert's first position
+  for (int e = wave; e < experts; e += 4) {
+    int run = first[e];
+    for (int b0 = 0; b0 < blocks; b0 += 64) {
+      const int b = b0 + lane;
+      const int c = b < blocks ? hist[int64_t(b) * experts + e] : 0;
+      int x = c;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+      }
+      if (b < blocks) hist[int64_t(b) * experts + e] = run + x - c;
+      run += __shfl(x, 63, 64);
+    }
+  }
 }
 
 // Position of every entry in the expert-sorted order: its block's first
@@ -326,8 +400,15 @@ void moe_w8(const MoeArgs& a) {
       const Epilogue lin{ENQ_ACT_LINEAR, 0.0f, 0.0f};
       dense_w8(a.x, a.tokens, a.d, a.wr, a.sr, E, a.br, lin, a.variant, logits, nullptr);
     }
-    moe_route_kernel<<<blocks_for(a.tokens), 256, 0, s>>>(logits, a.tokens, E, a.top_k, probs,
-                                                           chosen, gates);
+    if (E <= 8)
+      moe_route_regs_kernel<8><<<blocks_for(a.tokens), 256, 0, s>>>(logits, a.tokens, E, a.top_k,
+                                                                    probs, chosen, gates);
+    else if (E <= 32)
+      moe_route_regs_kernel<32><<<blocks_for(a.tokens), 256, 0, s>>>(logits, a.tokens, E,
+                                                                     a.top_k, probs, chosen, gates);
+    else
+      moe_route_kernel<<<blocks_for(a.tokens), 256, 0, s>>>(logits, a.tokens, E, a.top_k, probs,
+                                                             chosen, gates);
     check_launch("moe_route_kernel");
     moe_count_kernel<<<unsigned(sort_blocks), kSortBlock, 0, s>>>(chosen, entries, E, hist);
     check_launch("moe_count_kernel");

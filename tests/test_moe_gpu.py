@@ -71,7 +71,8 @@ def moe_model(rng, d, hidden, experts, top_k, activation="gelu", std=0.05, per_r
 
 
 @pytest.mark.parametrize("tokens,experts,top_k", [(8192, 8, 2), (1000, 4, 1), (37, 16, 4),
-                                                  (5, 3, 3)])
+                                                  (5, 3, 3), (300, 32, 5), (200, 40, 3),
+                                                  (20000, 8, 2)])
 def test_routing_from_logits(gpu, tokens, experts, top_k):
     print(f"[case] routing tokens={tokens} experts={experts} k={top_k}", flush=True)
     rng = np.random.default_rng(tokens + experts)
