@@ -78,6 +78,64 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
   }
 }
 
+// One wave per row, four rows per workgroup, for 16-byte aligned rows of at
+// most 64 * 4 * PER4 floats: float4 loads and reductions by wave shuffles
+// alone, with no workgroup barrier between the loads and the stores.
+template <int PER4>
+__global__ __launch_bounds__(256) void layernorm_wave_kernel(
+    const float* __restrict__ x, int64_t rows, int64_t cols, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, float* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // a whole wave
+  const int64_t nvec = cols / 4;
+  const float4* xr = reinterpret_cast<const float4*>(x + row * cols);
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  const float4* b4 = reinterpret_cast<const float4*>(beta);
+  float4* yr = reinterpret_cast<float4*>(y + row * cols);
+  // every load from an in-bounds address, masked where it is used
+  float4 v[PER4], gm[PER4], bt[PER4];
+#pragma unroll
+  for (int i = 0; i < PER4; ++i) {
+    const int64_t c = int64_t(i) * 64 + lane;
+    const int64_t cc = c < nvec ? c : 0;
+    v[i] = xr[cc];
+    gm[i] = g4[cc];
+    bt[i] = b4[cc];
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER4; ++i) {
+    const bool live = int64_t(i) * 64 + lane < nvec;
+    s += live ? (v[i].x + v[i].y) + (v[i].z + v[i].w) : 0.0f;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+  const float mean = s / float(cols);
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER4; ++i) {
+    const bool live = int64_t(i) * 64 + lane < nvec;
+    const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+    q += live ? (a * a + b * b) + (c * c + d * d) : 0.0f;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+  const float den = sqrtf(q / float(cols) + eps);
+#pragma unroll
+  for (int i = 0; i < PER4; ++i) {
+    const int64_t c = int64_t(i) * 64 + lane;
+    if (c < nvec) {
+      float4 o;
+      o.x = gm[i].x * ((v[i].x - mean) / den) + bt[i].x;
+      o.y = gm[i].y * ((v[i].y - mean) / den) + bt[i].y;
+      o.z = gm[i].z * ((v[i].z - mean) / den) + bt[i].z;
+      o.w = gm[i].w * ((v[i].w - mean) / den) + bt[i].w;
+      yr[c] = o;
+    }
+  }
+}
+
 // Rows longer than 256 * 16: the same arithmetic, re-reading the row.
 __global__ __launch_bounds__(256) void layernorm_long_kernel(const float* __restrict__ x,
                                                              int64_t cols,
@@ -369,7 +427,19 @@ extern "C" int enq_layernorm(const float* x, int64_t rows, int64_t cols, const f
     ENQ_REQUIRE(rows <= 0x7fffffff, "too many rows");
     const unsigned grid = unsigned(rows);
     hipStream_t s = stream();
-    if (cols <= 256 * 1)
+    const bool vec = cols % 4 == 0 && aligned(x, 16) && aligned(gamma, 16) &&
+                     aligned(beta, 16) && aligned(y, 16);
+    if (vec && cols <= 64 * 4 * 8) {
+      const unsigned g4 = unsigned(ceil_div(rows, int64_t(4)));
+      if (cols <= 64 * 4 * 1)
+        layernorm_wave_kernel<1><<<g4, 256, 0, s>>>(x, rows, cols, gamma, beta, eps, y);
+      else if (cols <= 64 * 4 * 2)
+        layernorm_wave_kernel<2><<<g4, 256, 0, s>>>(x, rows, cols, gamma, beta, eps, y);
+      else if (cols <= 64 * 4 * 4)
+        layernorm_wave_kernel<4><<<g4, 256, 0, s>>>(x, rows, cols, gamma, beta, eps, y);
+      else
+        layernorm_wave_kernel<8><<<g4, 256, 0, s>>>(x, rows, cols, gamma, beta, eps, y);
+    } else if (cols <= 256 * 1)
       layernorm_kernel<1><<<grid, 256, 0, s>>>(x, cols, gamma, beta, eps, y);
     else if (cols <= 256 * 2)
       layernorm_kernel<2><<<grid, 256, 0, s>>>(x, cols, gamma, beta, eps, y);

@@ -33,7 +33,7 @@ def row_rel_err(got, ref):
 
 
 @pytest.mark.parametrize("rows,cols", [(4096, 1024), (7, 5), (3, 300), (33, 1000), (2, 5000),
-                                       (5, 4096)])
+                                       (5, 4096), (6, 2048), (5, 1540)])
 def test_layernorm(gpu, rows, cols):
     print(f"[case] layernorm rows={rows} cols={cols}", flush=True)
     rng = np.random.default_rng(rows + cols)
