@@ -481,11 +481,21 @@ __global__ __launch_bounds__(kBlock) void finish_range_kernel(
   const int64_t c = blockIdx.x;
   Range<T> r;
   r.init();
-  const int64_t total = slices * inner;
-  for (int64_t k = threadIdx.x; k < total; k += kBlock) {
-    const int64_t s = k / inner, i = k - s * inner;
-    PartialRange<T> e = part[c * stride_c + s * stride_s + i];
-    r.merge(e.lo, e.hi, e.nan);
+  // min, max and the NaN flag merge exactly in any order
+  if (inner == 1) {
+    // no index division, and eight loads in flight per thread
+#pragma unroll 8
+    for (int64_t s = threadIdx.x; s < slices; s += kBlock) {
+      const PartialRange<T> e = part[c * stride_c + s * stride_s];
+      r.merge(e.lo, e.hi, e.nan);
+    }
+  } else {
+    const int64_t total = slices * inner;
+    for (int64_t k = threadIdx.x; k < total; k += kBlock) {
+      const int64_t s = k / inner, i = k - s * inner;
+      const PartialRange<T> e = part[c * stride_c + s * stride_s + i];
+      r.merge(e.lo, e.hi, e.nan);
+    }
   }
   wave_reduce(r);
   const int wave = threadIdx.x / 64;
