@@ -736,18 +736,26 @@ __global__ __launch_bounds__(kBlock) void elementwise_vec_kernel(
       const int64_t vi = v0 + int64_t(r) * kBlock;
       raw[r] = load_vec<T, V>(in + (vi < nfull ? vi : nfull - 1) * V);
     }
+    Vec<T, V> res[U];
+    int8_t codes[U][V];
 #pragma unroll
     for (int r = 0; r < U; ++r) {
       const int64_t vi = v0 + int64_t(r) * kBlock;
       T xs[V];
 #pragma unroll
       for (int e = 0; e < V; ++e) xs[e] = raw[r].v[e];
-      Vec<T, V> res;
-      int8_t codes[V];
-      apply(xs, vi < nfull ? vi * V : 0, vi < nfull ? V : 0, res, codes);
+      apply(xs, vi < nfull ? vi * V : 0, vi < nfull ? V : 0, res[r], codes[r]);
+    }
+    // every store after every load of the thread, so a wave's reads and
+    // writes reach HBM in separate bursts (storing each vector as its load
+    // arrived: 69.1 us against 65.3 for the per-tensor int8 codes pass)
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < U; ++r) {
+      const int64_t vi = v0 + int64_t(r) * kBlock;
       if (vi < nfull) {
-        if (out) store_vec<T, V>(out + vi * V, res);
-        if (OP == Op::kFakeTensor && out_codes) store_codes<V>(out_codes + vi * V, codes);
+        if (out) store_vec<T, V>(out + vi * V, res[r]);
+        if (OP == Op::kFakeTensor && out_codes) store_codes<V>(out_codes + vi * V, codes[r]);
       }
     }
   }
