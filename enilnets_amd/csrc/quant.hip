@@ -967,7 +967,7 @@ int grid_for(int64_t work_items, int per_cu = 8) {
   return int(blocks < 1 ? 1 : blocks);
 }
 
-constexpr int kElemUnroll = 4;  // vectors per thread of elementwise_vec_kernel
+constexpr int kElemUnroll = 4;  // vectors per thread of elementwise_vec_kernel (2: 4% slower, 8: 18%)
 
 template <class T, Op OP>
 void launch_elementwise(const void* in, int64_t n, int64_t channels, int64_t inner,
