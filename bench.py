@@ -3,24 +3,25 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-components] [--no-cpu]
 
-Headline (``value``): BASELINE.json configs[1], the 3-layer MLP
-784 -> 1024 -> 1024 -> 10 with per-output-channel int8 weights (He-normal
-fp32 init, biases ~N(0, 0.01)), ReLU hidden layers, batch 4096 of U(0, 1)
-activations.  One step is the three fused dequant-GEMMs of that batch on the
-fp32-accurate W8 path, inputs resident in HBM; the metric is the step's
-algorithmic TFLOP/s (2 * M * sum(N * K)).
+Headline (``value``): BASELINE.json configs[2], the largest single-GPU
+configuration: the W8 Dense of an 8192 x 8192 weight (N(0, 0.02), quantized
+per output channel to int8) on M = 4096 fp32 activations (N(0, 1)), on the
+fp32-accurate path (bf16 hi + lo activation planes on the matrix cores, fp32
+accumulation).  One step is one Dense call over that batch, inputs resident
+in HBM; the metric is the algorithmic TFLOP/s, 2 * M * N * K per step.
 
-``components`` reports the BASELINE configs[2] kernels (8192 x 8192 weight):
-quantize / dequantize GB/s, the M=16 GEMV, the M=4096 W8 GEMM in both
-variants, per-token activation quantization and the W8A8 int8 GEMM at
-M=4096 and 8192^3.  Memory-bound kernels rotate over enough buffers to
-exceed the 256 MB MALL, so their bytes come from HBM.  bench_vendor.py times
-the vendor library on the same GEMM shapes as a reference point.
+``components`` reports the other configs[2] kernels (quantize / dequantize
+GB/s, the M=16 GEMV, the bf16 variant, per-token activation quantization and
+the W8A8 int8 GEMM at M=4096 and 8192^3), the configs[1] MLP step, the
+configs[3] transformer block and the configs[4] MoE layer.  Memory-bound
+kernels rotate over enough buffers to exceed the 256 MB MALL, so their bytes
+come from HBM.
 
-``roofline`` is the dominant kernel of the headline step (the largest MLP
-layer's W8 GEMM), timed with HIP events on the library stream.
-``cpu_baseline`` times the NumPy oracle (the reference's CPU path, restated)
-on the host for a bounded sample of the same step.
+``roofline`` is the headline's one kernel, timed with HIP events on the
+library stream around the same calls.  ``cpu_baseline`` times the NumPy
+oracle (the reference's CPU path, restated) on the host on a bounded sample
+of the same workload: the fp32 Dense (BLAS sgemm on the fake-quantized
+weight) and the per-channel quantize / dequantize of the 8192 x 8192 weight.
 """
 
 import argparse
@@ -108,33 +109,85 @@ def build_mlp(rng):
     return m
 
 
-def cpu_threads():
+def host_info():
+    """The host that runs the CPU baseline: CPU model, logical CPUs, NumPy
+    and its BLAS (library, version, threads)."""
+    info = {"cpu_model": "unknown", "host_cpus": os.cpu_count(), "numpy": np.__version__,
+            "OPENBLAS_NUM_THREADS": os.environ.get("OPENBLAS_NUM_THREADS")}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    info["cpu_model"] = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     try:
         from threadpoolctl import threadpool_info
-        info = [i for i in threadpool_info() if i.get("user_api") == "blas"]
-        if info:
-            return int(info[0]["num_threads"])
+        for i in threadpool_info():
+            if i.get("user_api") == "blas":
+                info.update(blas=i.get("internal_api"), blas_version=i.get("version"),
+                            blas_threads=i.get("num_threads"))
+                break
     except Exception:
         pass
-    return os.cpu_count() or 1
+    return info
 
 
-def cpu_baseline(model, x, budget_s=12.0):
-    """The NumPy oracle's Dense chain (fake-quantized weights, fp32 sgemm) on
-    the host: median seconds per step over a bounded number of steps."""
-    import oracle
-    layers = model.layers
-    oracle.forward(layers, x[:256])          # warm-up
+def median_time(fn, budget_s, max_runs):
+    """Median seconds of ``fn()`` over up to ``max_runs`` runs within about
+    ``budget_s`` seconds (at least one run)."""
     times = []
     t_start = time.perf_counter()
-    while time.perf_counter() - t_start < budget_s and len(times) < 50:
+    while len(times) < max_runs and (not times or time.perf_counter() - t_start < budget_s):
         t0 = time.perf_counter()
-        oracle.forward(layers, x)
+        fn()
         times.append(time.perf_counter() - t0)
     return float(np.median(times)), len(times)
 
 
-def headline(args, timer, rng):
+def cpu_baseline(x, w, fq, codes, scale):
+    """The NumPy oracle on the host, on the headline's own inputs: the
+    reference's fp32 Dense (``np.dot(x, W.T) + b``, BLAS sgemm, on the
+    fake-quantized weight ``fq``) and the reference's per-channel
+    ``quantize_tensor`` of ``w`` and ``dequantize`` of its (float) codes.
+    About 10-20 s of host work."""
+    import oracle
+    M, K = x.shape
+    N = w.shape[0]
+    layer = {"type": "dense", "weights": fq, "bias": np.zeros(N, np.float32),
+             "activation": "linear"}
+    oracle.dense_forward(layer, x[:256])                       # warm-up (BLAS threads)
+    gemm_s, gemm_n = median_time(lambda: oracle.dense_forward(layer, x), 8.0, 5)
+    q_s, q_n = median_time(lambda: oracle.quantize_tensor(w, 8, "symmetric", per_channel=True),
+                           5.0, 3)
+    fcodes = codes.astype(np.float32)
+    zp = np.zeros_like(scale)
+    dq_s, dq_n = median_time(lambda: oracle.dequantize(fcodes, scale, zp), 3.0, 5)
+    fake_bytes = 8 * N * K + 8 * N          # fp32 in, fp32 out, scale + zero point
+    info = host_info()
+    return {
+        "value": round(2.0 * M * N * K / gemm_s / 1e12, 5), "unit": "TFLOP/s",
+        "cores": info.get("blas_threads") or info["host_cpus"], "kind": "port",
+        "sample": f"NumPy oracle on the headline's inputs: fp32 Dense {M}x{K} @ {N}x{K}^T "
+                  f"(BLAS sgemm on the fake-quantized weight), median of {gemm_n} calls; "
+                  f"per-channel quantize_tensor of the {N}x{K} weight, median of {q_n}; "
+                  f"dequantize of its float codes, median of {dq_n}",
+        "ms_per_step": round(gemm_s * 1e3, 3),
+        "quantize_per_channel": {"ms": round(q_s * 1e3, 2), "GB/s": round(fake_bytes / q_s / 1e9, 3),
+                                 "bytes": fake_bytes, "threads": 1,
+                                 "note": "fake-quantized floats out, as quantization.py:76-93 "
+                                         "returns them; NumPy ufuncs run on one core"},
+        "dequantize": {"ms": round(dq_s * 1e3, 2), "GB/s": round(fake_bytes / dq_s / 1e9, 3),
+                       "bytes": fake_bytes, "threads": 1,
+                       "note": "(q - zero_point) * scale on float codes (quantization.py:59-61)"},
+        "host": info,
+    }
+
+
+def mlp_step(timer, rng, steps, warmup):
+    """the three fused dequant-GEMMs of the MLP at batch
+    4096 (fp32-accurate W8), inputs resident in HBM."""
     from enilnets_amd.device import DeviceArray
     from enilnets_amd.nn import int8_weights
     from enilnets_amd.nn.dense import dense_w8
@@ -153,28 +206,59 @@ def headline(args, timer, rng):
             h = dense_w8(h, w, b, a, variant="fp32", out=o)
         return h
 
-    # correctness guard on a few rows against the oracle (float64 math)
-    y = step().numpy()
-    import oracle
-    ref = oracle.forward(model.layers, x[:64].astype(np.float64), dtype=np.float64)[-1]
-    rel = np.max(np.abs(y[:64] - ref)) / max(np.max(np.abs(ref)), 1e-30)
-    if not rel < 1e-3:
-        raise SystemExit(f"bench: MLP output differs from the oracle (rel {rel:.3e})")
-
     flops = 2.0 * M * sum(w.shape[0] * w.shape[1] for w in ws)
+    step()
+    for _ in range(warmup):
+        step()
+    ms = timer.time(step, steps)
+    # the largest layer's GEMM (4096 x 1024 x 1024), one kernel, timed alone
+    big = int(np.argmax([w.shape[0] * w.shape[1] for w in ws]))
+    h_in = d_x if big == 0 else outs[big - 1]
+    k_ms = timer.time(lambda i: dense_w8(h_in, ws[big], bs[big], acts[big], variant="fp32",
+                                         out=outs[big]), max(steps, 20))
+    k_flops = 2.0 * M * ws[big].shape[0] * ws[big].shape[1]
+    return {"mlp_step_config1": {
+        "ms": ms, "TFLOP/s": flops / ms / 1e9, "frac_bf16_peak": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
+        "gflop": flops / 1e9, "variant": "fp32",
+        "largest_layer": {"shape": [M, ws[big].shape[0], ws[big].shape[1]], "ms": k_ms,
+                          "TFLOP/s": k_flops / k_ms / 1e9,
+                          "frac_bf16_peak": k_flops / k_ms / 1e9 / BF16_PEAK_TFLOPS,
+                          "traffic": measured_traffic("mlp_layer_gemm",
+                                                      [M, ws[big].shape[0], ws[big].shape[1]])}}}
+
+
+def headline(args, timer, rng):
+    """BASELINE configs[2] at M = 4096: one fp32-accurate W8 Dense call per
+    step on the device-resident activations."""
+    from enilnets_amd.device import DeviceArray
+    from enilnets_amd.nn.dense import dense_w8, quantize_weight_rows
+    M, N, K = 4096, 8192, 8192
+    w = rng.normal(0.0, 0.02, (N, K)).astype(np.float32)
+    wq = rows = quantize_weight_rows(w)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    d_x = DeviceArray.from_numpy(x)
+    y = DeviceArray((M, N), np.float32)
+
+    def step(_=0):
+        dense_w8(d_x, wq, None, "linear", variant="fp32", out=y)
+
+    # correctness guard: 64 rows spread over the batch against float64 math
+    # on the fake-quantized weight (the tolerance of the parity tests)
+    step()
+    codes, scale = rows.codes.numpy(), rows.scale.numpy().reshape(-1, 1)
+    fq = codes.astype(np.float32) * scale          # dequantize: the fake-quantized weight
+    pick = np.arange(0, M, M // 64)
+    ref = x[pick].astype(np.float64) @ fq.astype(np.float64).T
+    got = y.numpy()[pick]
+    rel = np.max(np.abs(got - ref), axis=1) / np.max(np.abs(ref), axis=1)
+    if not np.all(rel <= 1e-4):
+        raise SystemExit(f"bench: W8 Dense differs from the oracle (max row error {rel.max():.3e})")
     for _ in range(args.warmup):
         step()
     ms = timer.time(step, args.steps)
-    # dominant kernel: the largest layer's GEMM, timed alone
-    big = int(np.argmax([w.shape[0] * w.shape[1] for w in ws]))
-    h_in = d_x if big == 0 else outs[big - 1]
-    w_big = ws[big]
-    reps = max(args.steps, 20)
-    k_ms = timer.time(lambda i: dense_w8(h_in, w_big, bs[big], acts[big], variant="fp32",
-                                         out=outs[big]), reps)
-    k_flops = 2.0 * M * w_big.shape[0] * w_big.shape[1]
-    return model, x, flops, ms, {"layer": big, "m": M, "n": w_big.shape[0],
-                                 "k": w_big.shape[1], "ms": k_ms, "flops": k_flops}
+    flops = 2.0 * M * N * K
+    return {"x": x, "w": w, "fq": fq, "codes": codes, "scale": scale, "m": M, "n": N, "k": K,
+            "ms": ms, "flops": flops}
 
 
 def components(timer, rng, only):
@@ -286,7 +370,8 @@ def components(timer, rng, only):
     x4 = DeviceArray.from_numpy(rng.standard_normal((M, K)).astype(np.float32))
     y4 = DeviceArray((M, N), np.float32)
     flops = 2.0 * M * nk
-    for variant in ("fp32", "bf16"):
+    # the fp32-accurate variant at this shape is the headline
+    for variant in ("bf16",):
         if on("gemm_" + variant):
             f = lambda i, v=variant: dense_w8(x4, wq[i % 2], None, "linear", variant=v, out=y4)
             f(0)
@@ -323,6 +408,8 @@ def components(timer, rng, only):
                                       "frac_int8_peak": tops / INT8_PEAK_TOPS}
         del xsq, ysq
     del wq, d_codes, d_scale, x4, y4
+    if on("mlp"):
+        out.update(mlp_step(timer, rng, 50, 10))
     if on("transformer_block"):
         out.update(transformer_block(timer, rng))
     if on("moe"):
@@ -568,12 +655,14 @@ def main():
           file=sys.stderr, flush=True)
     rng = np.random.default_rng(0)
     timer = Timer()
-    model, x, flops, ms, dom = headline(args, timer, rng)
-    print(f"[bench] MLP step {ms:.4f} ms", file=sys.stderr, flush=True)
+    h = headline(args, timer, rng)
+    ms, flops = h["ms"], h["flops"]
+    print(f"[bench] configs[2] W8 GEMM {ms:.4f} ms", file=sys.stderr, flush=True)
     value = flops / ms / 1e9
-    dom_tf = dom["flops"] / dom["ms"] / 1e9
+    shape = [h["m"], h["n"], h["k"]]
     result = {
-        "metric": "W8 Dense GEMM TFLOP/s (BASELINE configs[1] MLP step, fp32-accurate W8)",
+        "metric": "W8 Dense GEMM TFLOP/s (BASELINE configs[2]: 4096 x 8192 x 8192, "
+                  "fp32-accurate W8)",
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -584,32 +673,28 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 weights x fp32 activations (bf16 hi+lo MFMA, fp32 accumulate)",
-        "data": "synthetic (seeded He-normal weights, U(0,1) activations)",
-        "config": {"workload": "configs[1]: MLP 784-1024-1024-10, ReLU, batch 4096, "
-                               "per-output-channel int8 weights",
-                   "global_batch": 4096, "layers": 3, "variant": "fp32",
+        "data": "synthetic (seeded N(0, 0.02) weight quantized per output channel, "
+                "N(0, 1) activations)",
+        "config": {"workload": "configs[2]: Dense 8192x8192 int8 weight (per output channel), "
+                               "M=4096 fp32 activations, no bias, linear",
+                   "m": h["m"], "n": h["n"], "k": h["k"], "variant": "fp32",
                    "flops_per_step": flops},
-        "roofline": {"bound": "mfma", "kernel": "w8_ring_kernel<RingCfg<128,128,4,2,2,4,fused A>>",
-                     "shape": [dom["m"], dom["n"], dom["k"]],
-                     "achieved": round(dom_tf, 3), "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(dom_tf / BF16_PEAK_TFLOPS, 4),
-                     "traffic": measured_traffic("mlp_layer_gemm", [dom["m"], dom["n"], dom["k"]]),
-                     "note": "algorithmic 2*M*N*K over the measured time of the layer's "
-                             "dense call, one kernel that splits the fp32 activations "
-                             "itself; the fp32-accurate path issues two bf16 MFMA "
-                             "passes (hi, lo) per product, so its ceiling is half the "
+        "roofline": {"bound": "mfma",
+                     "kernel": "w8_ring_kernel<RingCfg<256,256,4,2,2,3,fused A>>",
+                     "shape": shape,
+                     "achieved": round(value, 3), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(value / BF16_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic("w8_gemm_config2", shape),
+                     "note": "algorithmic 2*M*N*K over the HIP-event time of the step, which "
+                             "is one launch of this kernel (it splits the fp32 activations "
+                             "into bf16 hi/lo itself); the fp32-accurate path issues two bf16 "
+                             "MFMA passes (hi, lo) per product, so its own ceiling is half the "
                              "bf16 peak"},
     }
     if not args.no_components:
         result["components"] = components(timer, rng, args.only)
     if not args.no_cpu:
-        sec, n = cpu_baseline(model, x)
-        result["cpu_baseline"] = {
-            "value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s", "cores": cpu_threads(),
-            "kind": "port",
-            "sample": f"NumPy oracle Dense chain (fake-quantized fp32 weights, BLAS sgemm), "
-                      f"full batch 4096, median of {n} steps",
-            "ms_per_step": round(sec * 1e3, 3)}
+        result["cpu_baseline"] = cpu_baseline(h["x"], h["w"], h["fq"], h["codes"], h["scale"])
     print(json.dumps(result))
     return 0
 

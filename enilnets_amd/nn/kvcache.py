@@ -25,7 +25,7 @@ import numpy as np
 
 from .. import _lib
 from ..device import DeviceArray, null
-from .dense import act_quant, act_quant_args, dense_w8
+from .dense import dense_w8
 from .forward import _FLOAT64_ACTIVATIONS, _bias
 from .moe import moe_forward
 from .transformer import MhaPlan, _at, _check_supported, embedding, layernorm, positional_encoding
@@ -210,9 +210,10 @@ def cached_forward_step(model: Any, inputs: Any, cache: KVCache, advance_positio
                 return w, _bias(layer, "bias", w.shape[0])
             w, b = _resources(cache, ("dense", idx), layer, make)
             dtype = np.float64 if layer["activation"] in _FLOAT64_ACTIVATIONS else np.float32
+            # no act_quant: the reference's cached step never fake-quantizes
+            # layer outputs (kvcache.py:84-118), calibrated or not
             x = dense_w8(x, w, b, layer["activation"],
-                         layer.get("activation_params", {}), variant,
-                         act_quant=layer.get("act_quant"), out_dtype=dtype)
+                         layer.get("activation_params", {}), variant, out_dtype=dtype)
         elif t == "dropout":
             pass
         elif t == "residual_save":
@@ -233,11 +234,6 @@ def cached_forward_step(model: Any, inputs: Any, cache: KVCache, advance_positio
             raise ValueError(
                 f"KV-cache stepping doesn't support layer type '{t}' (layer {idx}); use a full "
                 "Forward() for this architecture.")
-        spec = layer.get("act_quant")
-        if spec is not None and t not in ("dense",):
-            x = act_quant(x, spec, dtype)
-        if spec is not None:
-            dtype = act_quant_args(spec, dtype)[-1]
     if advance_position:
         cache.position += int(x.shape[1])
     out = x.numpy()

@@ -82,6 +82,37 @@ def test_dense_w8_large_gemv_and_gemm(gpu):
         assert np.all(row_rel_err(y[pick].astype(np.float64), ref) <= 1e-4)
 
 
+# 256 x 256 tiles (at least as many tiles as CUs): the kernel reads the fp32
+# activations and splits them itself; partial row and column tiles, a K tail
+# (K % 32 == 16), and activations at an address that is not 16-byte aligned
+# (the bf16 planes are then split in a separate pass)
+BIG_SHAPES = [(4096, 1024, 4096, 0), (4100, 1040, 4100, 0), (4097, 2048, 4095, 4),
+              (4096, 512, 4096, 4)]
+
+
+@pytest.mark.parametrize("m,k,n,offset", BIG_SHAPES)
+@pytest.mark.parametrize("variant,tol", [("fp32", 1e-4), ("bf16", 2e-2)])
+def test_dense_w8_big_tiles(gpu, m, k, n, offset, variant, tol):
+    print(f"[case] dense_w8 big {variant} m={m} k={k} n={n} offset={offset}", flush=True)
+    x, fq, codes, rows, b, wq = make(m, k, n, seed=m + k + n + offset, wstd=0.03)
+    if offset:
+        # the same activations one float past a 16-byte boundary
+        buf = DeviceArray.from_numpy(np.concatenate([np.zeros(offset // 4, np.float32),
+                                                     x.reshape(-1)]))
+        d_x = DeviceArray((m, k), np.float32, ptr=buf.address + offset, owner=buf)
+    else:
+        d_x = DeviceArray.from_numpy(x)
+    z = DeviceArray((m, n), np.float32)
+    y = D.dense_w8(d_x, wq, DeviceArray.from_numpy(b), "relu", variant=variant,
+                   pre_activation=z)
+    zh, yh = z.numpy(), y.numpy()
+    pick = np.unique(np.concatenate([np.arange(0, m, 37), np.arange(m - 5, m)]))
+    z_ref = x[pick].astype(np.float64) @ fq.astype(np.float64).T + b
+    err = row_rel_err(zh[pick].astype(np.float64), z_ref)
+    assert np.all(err <= tol), f"max row error {err.max():.3e} > {tol}"
+    assert np.array_equal(yh, np.maximum(zh, 0))
+
+
 @pytest.mark.parametrize("act", ["relu", "leakyrelu", "elu", "selu", "gelu", "swish", "mish",
                                  "sigmoid", "tanh", "softplus", "softmax"])
 def test_dense_w8_activations(gpu, act):

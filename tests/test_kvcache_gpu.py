@@ -90,6 +90,27 @@ def test_cached_steps_match_full_forward(gpu, window, moe):
         assert entry.start == 20 - entry.length
 
 
+def test_cached_steps_ignore_act_quant(gpu):
+    # the reference's cached step (kvcache.py:84-118) never applies a layer's
+    # act_quant spec: on a calibrated model the steps follow the float layers,
+    # while Forward fake-quantizes every layer output
+    print("[case] kvcache calibrated model", flush=True)
+    rng = np.random.default_rng(21)
+    m = decoder(rng)
+    tokens = rng.integers(0, 50, (2, 14))
+    cal = ea.ActivationCalibrator(m)
+    cal.observe(tokens)
+    cal.apply()
+    assert sum("act_quant" in layer for layer in m.layers) >= 8
+    stepped, _ = step_all(m, tokens, prime=6)
+    plain = [{k: v for k, v in layer.items() if k != "act_quant"} for layer in m.layers]
+    want = oracle.forward(plain, tokens, dtype=np.float64)[-1]
+    assert np.all(row_rel_err(stepped, want) <= 1e-4)
+    # the specs would have moved the outputs by about a grid step of each layer
+    quantized = oracle.forward(m.layers, tokens, dtype=np.float64)[-1]
+    assert np.max(row_rel_err(stepped, quantized)) > 1e-3
+
+
 def test_non_causal_attention_is_refused(gpu):
     m = decoder(np.random.default_rng(0), causal=False)
     with pytest.raises(ValueError):

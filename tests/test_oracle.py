@@ -493,3 +493,147 @@ def test_qat_observer_and_ste_mask_closed_forms():
     x = np.array([-1.0, -0.5, 0.0, 0.5, 1.0])
     m = oracle.ste_mask(x, 0.5 / 127, 0.0, 8, "symmetric")
     assert m.tolist() == [False, True, True, True, False]
+
+
+# ---------------------------------------------------------------------------
+# GELU: the tanh form of nn/activations.py:32, pinned at non-trivial points
+# against a 50-digit evaluation of the same formula, and shown to differ from
+# the erf form 0.5 x (1 + erf(x / sqrt 2)) there (x = 0 and large x cannot
+# tell the two apart).
+# ---------------------------------------------------------------------------
+_PI_50 = "3.14159265358979323846264338327950288419716939937510"
+
+
+def _gelu_tanh_decimal(x: float):
+    from decimal import Decimal, getcontext
+    getcontext().prec = 50
+    d = Decimal(x)
+    u = (Decimal(2) / Decimal(_PI_50)).sqrt() * (d + Decimal("0.044715") * d ** 3)
+    e2 = (2 * u).exp()
+    return Decimal("0.5") * d * (1 + (e2 - 1) / (e2 + 1))
+
+
+@pytest.mark.parametrize("x", [-3.0, -1.0, -0.5, 0.5, 1.0, 2.0, 3.0])
+def test_gelu_is_the_tanh_form(x):
+    import math
+    want = float(_gelu_tanh_decimal(x))
+    got = float(oracle.activate("gelu", np.array([x]))[0])
+    assert abs(got - want) <= 4e-16 * max(1.0, abs(want))
+    erf_form = 0.5 * x * (1 + math.erf(x / math.sqrt(2)))
+    assert abs(erf_form - want) > 1e-5
+    # a dropped cubic term moves the value by more than the bound as well
+    no_cubic = 0.5 * x * (1 + math.tanh(math.sqrt(2 / math.pi) * x))
+    assert abs(no_cubic - want) > 1e-5
+
+
+# ---------------------------------------------------------------------------
+# quantization_error (compression/quantization.py:218-229): closed forms.
+# ---------------------------------------------------------------------------
+def test_quantization_error_closed_forms():
+    import math
+    # one tensor: diff (1, -2), |a| = 5: relative = sqrt(5) / 5
+    r = oracle.quantization_error([np.array([3.0, 4.0])], [np.array([4.0, 2.0])])
+    assert r["mean_abs_error"] == 1.5
+    assert r["max_abs_error"] == 2.0
+    assert r["relative_error"] == pytest.approx(math.sqrt(5) / 5, rel=1e-15)
+    # a missing square root in the numerator (1.0) or the denominator
+    # (sqrt 5 / 25) would both miss this value
+    assert abs(r["relative_error"] - 1.0) > 0.1 and abs(r["relative_error"] - math.sqrt(5) / 25) > 0.1
+    # several outputs of different shapes are flattened and concatenated:
+    # a = (3, 4, 0, 12), b = (4, 2, 0, 12) -> diff (1, -2, 0, 0), |a| = 13
+    r = oracle.quantization_error([np.array([[3.0]]), np.array([4.0, 0.0]), np.array([[12.0]])],
+                                  [np.array([[4.0]]), np.array([2.0, 0.0]), np.array([[12.0]])])
+    assert r["mean_abs_error"] == 0.75
+    assert r["max_abs_error"] == 2.0
+    assert r["relative_error"] == pytest.approx(math.sqrt(5) / 13, rel=1e-15)
+    # a zero reference gives relative error 0 (the reference's denom > 0 branch)
+    r = oracle.quantization_error([np.zeros(3)], [np.array([1.0, -1.0, 2.0])])
+    assert r["relative_error"] == 0.0 and r["max_abs_error"] == 2.0
+    assert r["mean_abs_error"] == pytest.approx(4.0 / 3.0, rel=1e-15)
+
+
+# ---------------------------------------------------------------------------
+# forward (nn/forward.py:272-811): the layer loop, written out by hand.
+# outputs[0] is the input and layer i's output is outputs[i + 1] (:304,
+# :810); residual_add adds outputs[save_index] (:762-766); a layer's
+# act_quant fake-quantizes its output after the activation (:798-805).
+# ---------------------------------------------------------------------------
+def _chain_layers(rng):
+    def dense(n_in, n_out, act):
+        return {"type": "dense", "activation": act,
+                "weights": rng.standard_normal((n_out, n_in)) * 0.4,
+                "bias": rng.standard_normal(n_out) * 0.1}
+    spec = {"bits": 8, "scheme": "asymmetric", "scale": np.array(0.0123),
+            "zero_point": np.array(37.0)}
+    layers = [dense(6, 8, "relu"),                          # 0 -> outputs[1]
+              dense(8, 8, "tanh"),                          # 1 -> outputs[2]
+              {"type": "residual_add", "save_index": 1},    # 2 -> outputs[3]
+              {"type": "residual_save"},                    # 3 -> outputs[4]
+              {"type": "layernorm", "gamma": rng.standard_normal(8),
+               "beta": rng.standard_normal(8), "epsilon": 1e-5},   # 4
+              dense(8, 8, "linear"),                        # 5
+              {"type": "residual_add", "save_index": 4},    # 6: outputs[4]
+              dense(8, 5, "sigmoid")]                       # 7
+    layers[5]["act_quant"] = spec
+    layers[6]["act_quant"] = dict(spec, scale=np.array(0.05), zero_point=np.array(100.0))
+    return layers
+
+
+def _explicit_chain(layers, x, save_shift=0, skip_act_quant=False):
+    def fq(v, spec):
+        s, zp = float(spec["scale"]), float(spec["zero_point"])
+        q = np.clip(np.round(v / s + zp), 0, 255)
+        return (q - zp) * s
+
+    def sig(v):
+        return 1.0 / (1.0 + np.exp(-v))
+    W = [layer.get("weights") for layer in layers]
+    B = [layer.get("bias") for layer in layers]
+    o = [x]
+    o.append(np.maximum(0.0, x @ W[0].T + B[0]))
+    o.append(np.tanh(o[1] @ W[1].T + B[1]))
+    o.append(o[2] + o[1 + save_shift])
+    o.append(o[3])
+    g, b = layers[4]["gamma"], layers[4]["beta"]
+    mu = o[4].mean(axis=-1, keepdims=True)
+    var = ((o[4] - mu) ** 2).mean(axis=-1, keepdims=True)
+    o.append(g * (o[4] - mu) / np.sqrt(var + 1e-5) + b)
+    z5 = o[5] @ W[5].T + B[5]
+    o.append(z5 if skip_act_quant else fq(z5, layers[5]["act_quant"]))
+    r = o[6] + o[4 + save_shift]
+    o.append(r if skip_act_quant else fq(r, layers[6]["act_quant"]))
+    o.append(sig(o[7] @ W[7].T + B[7]))
+    return o
+
+
+def test_forward_matches_explicit_chain():
+    rng = np.random.default_rng(41)
+    layers = _chain_layers(rng)
+    x = rng.standard_normal((5, 6))
+    got = oracle.forward(layers, x, dtype=np.float64)
+    want = _explicit_chain(layers, x)
+    assert len(got) == len(layers) + 1 and got[0] is not None
+    for i, (g, w) in enumerate(zip(got, want)):
+        assert g.shape == w.shape, i
+        assert np.max(np.abs(g - w)) <= 1e-12, f"outputs[{i}]"
+    # the act_quant outputs sit on their grids
+    for i, li in ((6, 5), (7, 6)):
+        spec = layers[li]["act_quant"]
+        q = got[i] / float(spec["scale"]) + float(spec["zero_point"])
+        assert np.max(np.abs(q - np.round(q))) < 1e-9
+    # planted mistakes, each of which the comparison above would catch: a
+    # save_index read one output later, act_quant left out, and (below)
+    # act_quant applied before a non-linear activation instead of after it
+    for kw in ({"save_shift": 1}, {"skip_act_quant": True}):
+        bad = _explicit_chain(layers, x, **kw)
+        assert max(np.max(np.abs(g - w)) for g, w in zip(got, bad)) > 1e-3, kw
+    tl = _chain_layers(np.random.default_rng(41))
+    tl[5]["activation"] = "tanh"
+    got_t = oracle.forward(tl, x, dtype=np.float64)
+    z = got_t[5] @ tl[5]["weights"].T + tl[5]["bias"]
+    spec = tl[5]["act_quant"]
+    s, zp = float(spec["scale"]), float(spec["zero_point"])
+    after = (np.clip(np.round(np.tanh(z) / s + zp), 0, 255) - zp) * s
+    before = np.tanh((np.clip(np.round(z / s + zp), 0, 255) - zp) * s)
+    assert np.max(np.abs(got_t[6] - after)) <= 1e-12
+    assert np.max(np.abs(got_t[6] - before)) > 1e-3

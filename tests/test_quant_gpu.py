@@ -226,17 +226,71 @@ def test_int8_rows(gpu, shape):
     same_bits(scale.numpy(), want_scale.reshape(-1))
 
 
-def test_dequantize_i8(gpu):
+# (outer, channels, inner) layouts of enq_dequantize_i8: per-channel rows,
+# per-tensor (one channel), a middle channel axis; shapes with n % 4 == 0 and
+# inner % 4 == 0 take dequant_i8_kernel, the rest the elementwise kernel
+DEQUANT_LAYOUTS = [(1, 33, 70), (1, 64, 1024), (1, 8192, 256), (1, 1, 65536), (1, 1, 1003),
+                   (3, 5, 64), (2, 7, 9), (1, 8192, 8192)]
+
+
+@pytest.mark.parametrize("outer,channels,inner", DEQUANT_LAYOUTS)
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_dequantize_i8(gpu, outer, channels, inner, dtype):
+    from enilnets_amd import _lib
+    if outer * channels * inner > 1 << 24 and dtype == np.float64:
+        pytest.skip("the float32 case covers the full-size layout")
+    print(f"[case] dequantize_i8 {outer}x{channels}x{inner} {np.dtype(dtype).name}", flush=True)
+    rng = np.random.default_rng(channels + inner)
+    codes = rng.integers(-127, 128, (outer, channels, inner), dtype=np.int8)
+    scale = (rng.uniform(0.5, 2.0, (1, channels, 1)) * 0.01).astype(dtype)
+    d_c, d_s = DeviceArray.from_numpy(codes), DeviceArray.from_numpy(scale.reshape(-1))
+    out = DeviceArray(codes.shape, dtype)
+    code = _lib.F32 if dtype == np.float32 else _lib.F64
+    _lib.call("enq_dequantize_i8", code, d_c.ptr, outer, channels, inner, d_s.ptr, out.ptr)
+    want = oracle.dequantize(codes.astype(dtype), scale, np.zeros_like(scale))
+    assert want.dtype == dtype
+    assert np.array_equal(out.numpy(), want)   # == semantics: int8 0 gives +0.0
+
+
+def test_dequantize_i8_unaligned_output(gpu):
+    # an output that is not 16-byte aligned takes the elementwise kernel on
+    # purpose; the values are the same
     import ctypes
     from enilnets_amd import _lib
-    rng = np.random.default_rng(12)
-    w = rng.standard_normal((33, 70)).astype(np.float32)
-    codes, scale = oracle.int8_codes(w, per_channel=True)
-    d_c, d_s = DeviceArray.from_numpy(codes), DeviceArray.from_numpy(scale.reshape(-1))
-    out = DeviceArray(codes.shape, np.float32)
-    _lib.call("enq_dequantize_i8", _lib.F32, d_c.ptr, 1, 33, 70, d_s.ptr, out.ptr)
-    want = oracle.dequantize(codes.astype(np.float32), scale, np.zeros_like(scale))
-    assert np.array_equal(out.numpy(), want)   # == semantics: int8 0 gives +0.0
+    rng = np.random.default_rng(13)
+    codes = rng.integers(-127, 128, (64, 1024), dtype=np.int8)
+    scale = (rng.uniform(0.5, 2.0, 64) * 0.01).astype(np.float32)
+    d_c, d_s = DeviceArray.from_numpy(codes), DeviceArray.from_numpy(scale)
+    buf = DeviceArray.from_numpy(np.zeros(codes.size + 4, np.float32))
+    _lib.call("enq_dequantize_i8", _lib.F32, d_c.ptr, 1, 64, 1024, d_s.ptr,
+              ctypes.c_void_p(buf.address + 4))
+    got = buf.numpy()
+    want = oracle.dequantize(codes.astype(np.float32), scale.reshape(-1, 1), np.float32(0))
+    assert np.array_equal(got[1:1 + codes.size].reshape(codes.shape), want)
+    assert got[0] == 0 and not got[1 + codes.size:].any()
+
+
+def test_quantize_tensor_per_channel_8192(gpu):
+    # BASELINE configs[2]'s weight through the public API (row kernel) and
+    # its int8 codes, bit-exact; the codes dequantize back to the fake floats
+    from enilnets_amd import _lib
+    from enilnets_amd.nn.dense import quantize_weight_rows
+    print("[case] quantize_tensor per channel 8192x8192", flush=True)
+    rng = np.random.default_rng(8192)
+    w = rng.normal(0.0, 0.02, (8192, 8192)).astype(np.float32)
+    got = ea.quantize_tensor(w, 8, "symmetric", per_channel=True)
+    want = oracle.quantize_tensor(w, 8, "symmetric", per_channel=True)
+    assert np.array_equal(got[0], want[0])
+    same_bits(got[1], want[1])
+    same_bits(got[2], want[2])
+    rows = quantize_weight_rows(w)
+    want_codes, want_scale = oracle.int8_codes(w, per_channel=True)
+    assert np.array_equal(rows.codes.numpy(), want_codes)
+    same_bits(rows.scale.numpy(), want_scale.reshape(-1))
+    out = DeviceArray(w.shape, np.float32)
+    _lib.call("enq_dequantize_i8", _lib.F32, rows.codes.ptr, 1, 8192, 8192, rows.scale.ptr,
+              out.ptr)
+    assert np.array_equal(out.numpy(), want[0])
 
 
 @pytest.mark.parametrize("shape", [(64, 48), (1024, 784), (10, 1024), (300, 2000), (33, 9000)])
