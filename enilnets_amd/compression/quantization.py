@@ -372,8 +372,8 @@ class ActivationCalibrator:
             if self.percentile is None:
                 low, high = _global_range(out)
             else:
-                raise NotImplementedError(
-                    "percentile calibration is not implemented on the GPU path")
+                p = self.percentile
+                low, high = _percentiles(out, (100.0 - p, p))
             if i in self.ranges:
                 self.ranges[i] = [min(self.ranges[i][0], low), max(self.ranges[i][1], high)]
             else:
@@ -403,6 +403,60 @@ def _global_range(x: np.ndarray) -> Tuple[float, float]:
     d_lo, d_hi = DeviceArray((1,), a.dtype), DeviceArray((1,), a.dtype)
     _lib.call("enq_minmax", code, d_x.ptr, 1, 1, a.size, d_lo.ptr, d_hi.ptr)
     return float(d_lo.numpy()[0]), float(d_hi.numpy()[0])
+
+
+def _percentiles(x: np.ndarray, qs: Sequence[float]) -> List[float]:
+    """``float(np.percentile(x, q))`` for each q (NumPy's default 'linear'
+    method), as the calibrator's ``quantization.py:186-187`` takes them.
+
+    The order statistics come from ``enq_order_stats`` (a device radix
+    select); around them this follows NumPy 2's ``_quantile``: q / 100 and
+    the virtual index ``(n - 1) * q`` in the array's float type, the two
+    neighbouring ranks (both the last one past the end), and the two-sided
+    interpolation of ``_lerp`` (``a + d * t``, or ``b - d * (1 - t)`` for
+    ``t >= 0.5``) in that type; a NaN anywhere gives NaN."""
+    a = np.ascontiguousarray(x).reshape(-1)
+    if a.dtype not in (np.float32, np.float64):
+        raise NotImplementedError(f"percentile calibration takes float32 or float64, got {a.dtype}")
+    n = a.size
+    if n == 0:
+        raise IndexError("index -1 is out of bounds for axis 0 with size 0")
+    t = a.dtype.type
+    plans = []
+    for q in qs:
+        frac = np.asanyarray(np.true_divide(q, t(100)))
+        if not 0.0 <= frac <= 1.0:
+            raise ValueError("Percentiles must be in the range [0, 100]")
+        vi = np.asanyarray((n - 1) * frac)
+        # NumPy's indexes: -1 (the last element) for both at or past the end,
+        # and gamma taken against that -1
+        if vi >= n - 1:
+            lo_i = hi_i = -1
+        elif vi < 0:
+            lo_i = hi_i = 0
+        else:
+            lo_i = int(np.floor(vi))
+            hi_i = lo_i + 1
+        gamma = np.asanyarray(vi - np.intp(lo_i), dtype=vi.dtype)
+        plans.append((lo_i % n, hi_i % n, gamma))
+    ranks = sorted({r for lo_i, hi_i, _ in plans for r in (lo_i, hi_i)} | {n - 1})
+    d_x = DeviceArray.from_numpy(a)
+    d_out = DeviceArray((len(ranks),), a.dtype)
+    host_ranks = (ctypes.c_int64 * len(ranks))(*ranks)
+    _lib.call("enq_order_stats", _compute_code(a.dtype), d_x.ptr, n, host_ranks, len(ranks),
+              d_out.ptr)
+    vals = dict(zip(ranks, d_out.numpy()))
+    if np.isnan(vals[n - 1]):           # NaN sorts last: any NaN makes every result NaN
+        return [float("nan")] * len(plans)
+    result = []
+    for lo_i, hi_i, gamma in plans:
+        lo, hi = np.asanyarray(vals[lo_i]), np.asanyarray(vals[hi_i])
+        diff = np.subtract(hi, lo)
+        v = np.asanyarray(np.add(lo, diff * gamma))
+        if gamma >= 0.5:
+            v = np.asanyarray(np.subtract(hi, diff * (1 - gamma)), dtype=v.dtype)
+        result.append(float(v))
+    return result
 
 
 def remove_activation_quantization(model: Any) -> None:

@@ -196,6 +196,16 @@ int enq_dequantize_i8(int dtype, const int8_t* codes, int64_t outer,
 int enq_error_stats(int dtype, const void* reference, const void* candidate,
                     int64_t n, double* host_out4);
 
+/* Order statistics for ActivationCalibrator(percentile=p)
+ * (quantization.py:183-188, np.percentile(out, 100 - p) and
+ * np.percentile(out, p)): out[i] = the element at position host_ranks[i]
+ * (0 <= rank < n) of x (n elements of dtype) sorted ascending, NaN after
+ * every number, as np.partition places it.  out is device memory of count
+ * elements.  The host forms NumPy's 'linear' virtual index and interpolates
+ * between the two order statistics around it. */
+int enq_order_stats(int dtype, const void* x, int64_t n, const int64_t* host_ranks,
+                    int count, void* out);
+
 /* ---- Dense on int8 weights -----------------------------------------
  * y = act(x . (codes * w_scale)^T + bias) with x (m, k) fp32, codes (n, k)
  * int8, w_scale (n) fp32, bias (n) fp32 or NULL, y (m, n) fp32.
@@ -209,6 +219,7 @@ int enq_dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes,
                  const float* w_scale, int64_t n, const float* bias,
                  int activation, float act_alpha, float act_clip, int variant,
                  float* y, float* z);
+
 
 /* enq_dense_w8 followed, in the same epilogue, by the activation
  * fake-quantization of forward.py:798-805 (act_quant spec of a calibrated

@@ -18,6 +18,7 @@ from .quantization import (QUANTIZABLE, compute_scale, dequantize,
                            quantize, quantize_tensor, quantize_weights,
                            int8_codes)
 from .qat import MovingRange, qat_linear_forward, qat_quantized_weight, ste_mask
+from .calibration import observe_ranges, percentile, specs_from_ranges
 from .forward import (activate, dense_forward, forward, forward_top_k, layernorm_forward,
                       mha_forward, moe_forward, router, top_k, w8a8_dense, window_mask)
 
@@ -27,5 +28,5 @@ __all__ = [
     "quantize_weights", "int8_codes", "activate", "dense_forward", "forward",
     "layernorm_forward", "mha_forward", "moe_forward", "w8a8_dense", "forward_top_k",
     "router", "top_k", "window_mask", "MovingRange", "qat_linear_forward",
-    "qat_quantized_weight", "ste_mask",
+    "qat_quantized_weight", "ste_mask", "observe_ranges", "percentile", "specs_from_ranges",
 ]

@@ -136,3 +136,72 @@ def test_forward_with_calibrated_activations(gpu):
         assert off.mean() < 2e-2, f"layer {i}: {off.mean():.2e} of outputs off the oracle's grid point"
     ea.remove_activation_quantization(m)
     assert all("act_quant" not in L for L in m.layers)
+
+
+# ---------------------------------------------------------------------------
+# Percentile calibration (quantization.py:183-188): the device order
+# statistics with NumPy's 'linear' interpolation give np.percentile's value
+# bit for bit (== semantics: -0.0 and +0.0 are equal, as NumPy's sort
+# treats them).
+# ---------------------------------------------------------------------------
+def _percentile_cases():
+    rng = np.random.default_rng(5)
+    ties = rng.integers(-3, 4, 5000).astype(np.float32)
+    zeros = np.array([0.0, -0.0, 1.0, -0.0, 0.0, -1.0], np.float32)
+    inf = rng.standard_normal(300).astype(np.float32)
+    inf[[3, 70]] = [np.inf, -np.inf]
+    nan = rng.standard_normal(100).astype(np.float32)
+    nan[17] = np.nan
+    return [("one", np.array([2.5], np.float32)), ("two", np.array([1.0, -4.0], np.float64)),
+            ("normal", rng.standard_normal((64, 1000)).astype(np.float32)),
+            ("normal64", rng.standard_normal(70001)), ("ties", ties), ("zeros", zeros),
+            ("inf", inf), ("nan", nan),
+            ("relu", np.maximum(rng.standard_normal(1 << 20), 0).astype(np.float32)),
+            # past 2^24 elements the float32 virtual index rounds, as NumPy's does
+            ("big", rng.standard_normal((1 << 24) + 5).astype(np.float32))]
+
+
+@pytest.mark.parametrize("case", range(10))
+def test_percentile_matches_numpy(gpu, case):
+    from enilnets_amd.compression.quantization import _percentiles
+    name, x = _percentile_cases()[case]
+    print(f"[case] percentile {name} n={x.size}", flush=True)
+    qs = (0.0, 0.1, 1.0, 37.5, 50.0, 99.0, 99.9, 100.0)
+    got = _percentiles(x, qs)
+    for q, g in zip(qs, got):
+        want = oracle.percentile(x, q)
+        assert (np.isnan(g) and np.isnan(want)) or g == want, (name, q, g, want)
+
+
+def test_percentile_calibration(gpu):
+    # ActivationCalibrator(percentile=p) over two batches: ranges and specs
+    # identical to the reference's observe / apply on the same layer outputs
+    rng = np.random.default_rng(44)
+    m = Model()
+    m.add_dense((rng.standard_normal((256, 100)) * 0.1).astype(np.float32),
+                (rng.standard_normal(256) * 0.01).astype(np.float32), "relu")
+    m.add_dense((rng.standard_normal((64, 256)) * 0.1).astype(np.float32),
+                (rng.standard_normal(64) * 0.01).astype(np.float32), "gelu")
+    ea.quantize_weights(m, per_channel=True)
+    for p in (99.9, 95.0):
+        cal = ea.ActivationCalibrator(m, percentile=p)
+        ranges = {}
+        for seed in (1, 2):
+            x = np.random.default_rng(seed).uniform(0, 1, (300, 100)).astype(np.float32)
+            cal.observe(x)
+            ranges = oracle.observe_ranges(m.outputs, percentile_p=p, ranges=ranges)
+        assert cal.ranges == ranges
+        installed = cal.apply()
+        want = oracle.specs_from_ranges(ranges)
+        for i in want:
+            for key in ("scale", "zero_point", "low", "high"):
+                assert np.array_equal(installed[i][key], want[i][key]), (p, i, key)
+        # a clipped range lies inside the full one over the same batches
+        ea.remove_activation_quantization(m)
+        full = ea.ActivationCalibrator(m)
+        for seed in (1, 2):
+            full.observe(np.random.default_rng(seed).uniform(0, 1, (300, 100)).astype(np.float32))
+        for i in ranges:
+            assert full.ranges[i][0] <= ranges[i][0] <= ranges[i][1] <= full.ranges[i][1]
+    with pytest.raises(ValueError):
+        ea.ActivationCalibrator(m, percentile=101.0).observe(x)

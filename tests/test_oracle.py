@@ -637,3 +637,57 @@ def test_forward_matches_explicit_chain():
     before = np.tanh((np.clip(np.round(z / s + zp), 0, 255) - zp) * s)
     assert np.max(np.abs(got_t[6] - after)) <= 1e-12
     assert np.max(np.abs(got_t[6] - before)) > 1e-3
+
+
+# ---------------------------------------------------------------------------
+# Calibration ranges (compression/quantization.py:176-209).  The percentile
+# path is NumPy's np.percentile (default 'linear' method): pinned against the
+# exact rational interpolation between the two order statistics around
+# (n - 1) q / 100, and closed forms on integer ramps.
+# ---------------------------------------------------------------------------
+def _exact_percentile(values, q):
+    # the virtual index as the method defines it on floats, (n - 1) * (q / 100)
+    # in float64; the interpolation between the order statistics exact
+    s = sorted(Fraction(float(v)) for v in values)
+    h = Fraction((len(s) - 1) * (q / 100.0))
+    lo = int(h)
+    if lo >= len(s) - 1:
+        return s[-1]
+    return s[lo] + (h - lo) * (s[lo + 1] - s[lo])
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 17, 1000])
+def test_percentile_is_linear_interpolation(n):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n)
+    for q in (0.0, 0.1, 12.5, 50.0, 99.0, 99.9, 100.0):
+        got = oracle.percentile(x, q)
+        want = _exact_percentile(x, q)
+        ulp = np.spacing(max(abs(float(want)), 1e-300))
+        assert abs(Fraction(got) - want) <= 4 * Fraction(float(ulp)), (n, q)
+    # an integer ramp: the percentile is the index itself
+    ramp = np.arange(101, dtype=np.float64)
+    for q in (0, 1, 37, 50, 99, 100):
+        assert oracle.percentile(ramp, q) == q
+    assert np.isnan(oracle.percentile(np.array([1.0, np.nan, 3.0]), 50))
+
+
+def test_observe_ranges_and_specs():
+    rng = np.random.default_rng(2)
+    outs = [rng.standard_normal((8, 3)), rng.standard_normal((8, 4)) * 3,
+            np.arange(6, dtype=np.int64), rng.uniform(0, 1, (8, 2))]
+    r = oracle.observe_ranges(outs)
+    assert sorted(r) == [0, 2]          # the integer output is skipped
+    assert r[0] == [float(outs[1].min()), float(outs[1].max())]
+    r = oracle.observe_ranges(outs, percentile_p=90.0)
+    assert r[0] == [float(np.percentile(outs[1], 10.0)), float(np.percentile(outs[1], 90.0))]
+    # a second batch widens the ranges
+    wider = [o * 2 if o.dtype.kind == "f" else o for o in outs]
+    r2 = oracle.observe_ranges(wider, percentile_p=90.0, ranges={k: list(v) for k, v in r.items()})
+    for k in r:
+        assert r2[k][0] == min(r[k][0], 2 * r[k][0]) and r2[k][1] == max(r[k][1], 2 * r[k][1])
+    specs = oracle.specs_from_ranges(r)
+    low, high = r[2]
+    assert float(specs[2]["scale"]) == float(np.float64(high - low) / 255)
+    with pytest.raises(RuntimeError):
+        oracle.specs_from_ranges({})
