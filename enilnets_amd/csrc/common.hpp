@@ -69,6 +69,14 @@ constexpr int kKernelSlot = 0;
 constexpr int kLayerSlot = 1;
 void* workspace(size_t bytes, int slot = kKernelSlot);
 
+// Fixed device scratch of the allocation-free entry point
+// (enq_dense_w8_noalloc): a file-scope device array, one copy per device,
+// whose address enq_init looks up once per device.  Returns the current
+// device's copy; fails with ENQ_ERR_INVALID when `bytes` exceeds it.  It
+// allocates nothing, and every call on a device shares the one array.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+void* noalloc_scratch(size_t bytes);
+
 // Checks the launch that was just enqueued.
 void check_launch(const char* what);
 

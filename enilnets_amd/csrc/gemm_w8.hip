@@ -1237,7 +1237,8 @@ void dense_w8_grouped(const uint16_t* xa, int64_t plane_stride, int64_t kp, int 
 
 void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const float* w_scale,
               int64_t n, const float* bias, const Epilogue& ep_all, int variant, float* y,
-              float* z) {
+              float* z, bool no_alloc) {
+  auto scratch_of = [&](size_t bytes) { return no_alloc ? noalloc_scratch(bytes) : workspace(bytes); };
   const int planes = variant == ENQ_W8_FP32 ? 2 : 1;
   // split-K GEMV for few activation rows, and for tall-skinny outputs (one
   // 16-row block per grid z index, so at most 65535 * 16 rows); both read
@@ -1273,7 +1274,7 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
   const Epilogue ep = gemm_epilogue(ep_all, fuse_aq);
   if (gemv) {
     const GemvPlan plan = plan_gemv(m, n, k);
-    auto* part = static_cast<float*>(workspace(plan.part_bytes(n)));
+    auto* part = static_cast<float*>(scratch_of(plan.part_bytes(n)));
     // 128-wide K chunks need per-chunk guards unless k is a multiple of 128
     const int km = kmode == 0 ? (k % 128 == 0 ? 0 : 1) : kmode;
     with_modes(km, [&](auto planes_tag, auto kmode_tag) {
@@ -1302,7 +1303,7 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
     } else {
       const int64_t plane_stride = m * kp;
       auto* xa =
-          static_cast<uint16_t*>(workspace(size_t(planes) * plane_stride * sizeof(uint16_t)));
+          static_cast<uint16_t*>(scratch_of(size_t(planes) * plane_stride * sizeof(uint16_t)));
       split_planes(x, nullptr, m, k, xa, m, kp, planes);
       with_modes(kmode, [&](auto planes_tag, auto kmode_tag) {
         gemm_dispatch<decltype(planes_tag)::value, decltype(kmode_tag)::value>(
@@ -1329,6 +1330,22 @@ extern "C" int enq_dense_w8(const float* x, int64_t m, int64_t k, const int8_t* 
     ENQ_REQUIRE(variant == ENQ_W8_FP32 || variant == ENQ_W8_BF16, "unknown variant %d", variant);
     Epilogue ep{activation, act_alpha, act_clip};
     dense_w8(x, m, k, codes, w_scale, n, bias, ep, variant, y, z);
+  });
+}
+
+extern "C" int enq_dense_w8_noalloc(const float* x, int64_t m, int64_t k, const int8_t* codes,
+                                    const float* w_scale, int64_t n, const float* bias,
+                                    int activation, float act_alpha, float act_clip, int variant,
+                                    float* y, float* z) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && n >= 1 && k >= 1, "m, n, k must be positive (m=%lld n=%lld k=%lld)",
+                (long long)m, (long long)n, (long long)k);
+    ENQ_REQUIRE(x && codes && w_scale && y, "NULL pointer argument");
+    ENQ_REQUIRE(valid_activation(activation), "unknown activation code %d", activation);
+    ENQ_REQUIRE(variant == ENQ_W8_FP32 || variant == ENQ_W8_BF16, "unknown variant %d", variant);
+    Epilogue ep{activation, act_alpha, act_clip};
+    dense_w8(x, m, k, codes, w_scale, n, bias, ep, variant, y, z, /*no_alloc=*/true);
   });
 }
 

@@ -11,9 +11,11 @@
 namespace enq {
 
 // act(x @ (codes * w_scale).T + bias), fp32 x of shape (m, k); z receives the
-// pre-activation when non-null.  Uses the kernel workspace slot.
+// pre-activation when non-null.  Uses the kernel workspace slot, or with
+// `no_alloc` the fixed scratch (noalloc_scratch), checked before any launch.
 void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const float* w_scale,
-              int64_t n, const float* bias, const Epilogue& ep, int variant, float* y, float* z);
+              int64_t n, const float* bias, const Epilogue& ep, int variant, float* y, float* z,
+              bool no_alloc = false);
 
 // x rows (gathered through `gather` when non-null) -> `planes` bf16 planes of
 // shape (mp, kp), zero padded; plane p starts at xa + p * mp * kp.

@@ -26,6 +26,14 @@ struct DeviceState {
 DeviceState g_state;
 std::mutex g_mutex;
 
+// The allocation-free entry point's scratch.  Host code never uses this name
+// as an address (on the host it is only a stand-in for the symbol): enq_init
+// asks the runtime for the array's address on each device it sets up, and
+// noalloc_scratch hands out that address.
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+void* g_scratch_addr[kMaxDevices] = {};
+
 // Caching device allocator behind enq_malloc / enq_free.  Every kernel and
 // copy of the library runs in order on one stream, so a freed block can be
 // handed out again at once: whatever is enqueued on it next runs after the
@@ -119,6 +127,15 @@ void* workspace(size_t bytes, int slot) {
   return g_state.workspace[slot];
 }
 
+void* noalloc_scratch(size_t bytes) {
+  ENQ_REQUIRE(bytes <= kNoAllocScratchBytes,
+              "needs %zu bytes of scratch; the allocation-free entry point has %zu (64 MiB)",
+              bytes, kNoAllocScratchBytes);
+  void* p = g_scratch_addr[g_state.device];
+  if (p == nullptr) fail(ENQ_ERR_RUNTIME, "scratch of device %d not set up", g_state.device);
+  return p;
+}
+
 void check_launch(const char* what) {
   hipError_t err = hipGetLastError();
   if (err != hipSuccess)
@@ -158,7 +175,15 @@ int enq_init(int device) {
         if (w) ENQ_HIP(hipFree(w));
       g_state = DeviceState{};
     }
+    if (device >= kMaxDevices)
+      fail(ENQ_ERR_INVALID, "device %d beyond the %d this library tracks", device, kMaxDevices);
     ENQ_HIP(hipSetDevice(device));
+    if (g_scratch_addr[device] == nullptr) {
+      // once per device, with that device current: its own copy of the array
+      void* p = nullptr;
+      ENQ_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+      g_scratch_addr[device] = p;
+    }
     hipStream_t s = nullptr;
     // Default priority on purpose: streams of mixed priority are avoided.
     ENQ_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
