@@ -1265,11 +1265,6 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
   // fake-quantization; the other GEMM kernels leave it to finish_rows
   const bool big = ceil_div(m, 256) * ceil_div(n, 256) >= device_cu_count();
   const bool fused_mid = !gemv && !big && kmode != 2 && k % 4 == 0 && aligned(x, 16);
-  // the 256 x 256 kernel takes the fp32 activations itself on the
-  // fp32-accurate path only: a bf16 variant reading fp32 rows moves twice the
-  // LDS bytes of its one bf16 plane (4096 x 8192 x 8192: 0.72 against 0.58 ms)
-  const bool fused_big = !gemv && big && planes == 2 && kmode != 2 && k % 4 == 0 &&
-                         aligned(x, 16);
   const bool fuse_aq = gemv || fused_mid;
   const Epilogue ep = gemm_epilogue(ep_all, fuse_aq);
   if (gemv) {
@@ -1295,12 +1290,13 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
         launch_w8_ring<RingCfg<128, 128, 4, 2, P, 4, true>>(nullptr, 0, kp, codes, w_scale, bias,
                                                             m, n, k, ep, y, z, RowGroups{}, x);
       });
-    } else if (fused_big) {
-      // fp32-accurate 4096 x 8192 x 8192: 1.041 ms against 1.056 for the
-      // separate split pass and the two-plane kernel
-      launch_w8_ring<RingCfg<256, 256, 4, 2, 2, 3, true>>(nullptr, 0, kp, codes, w_scale, bias,
-                                                          m, n, k, ep, y, z, RowGroups{}, x);
     } else {
+      // Large GEMMs split the activations in a pass of their own.  Splitting
+      // them inside the 256 x 256 kernel instead (as the 128 x 128 kernel
+      // does) issues 64 more VALU instructions per wave per 16-deep k-step,
+      // which the SIMD does not overlap with its MFMAs: 4096 x 8192 x 8192
+      // took 1.167 against 1.048-1.068 ms (split pass included) on one box,
+      // 1.041 against 1.056 on another.
       const int64_t plane_stride = m * kp;
       auto* xa =
           static_cast<uint16_t*>(scratch_of(size_t(planes) * plane_stride * sizeof(uint16_t)));
@@ -1330,6 +1326,58 @@ extern "C" int enq_dense_w8(const float* x, int64_t m, int64_t k, const int8_t* 
     ENQ_REQUIRE(variant == ENQ_W8_FP32 || variant == ENQ_W8_BF16, "unknown variant %d", variant);
     Epilogue ep{activation, act_alpha, act_clip};
     dense_w8(x, m, k, codes, w_scale, n, bias, ep, variant, y, z);
+  });
+}
+
+extern "C" int enq_split_planes(const float* x, int64_t m, int64_t k, int variant,
+                                uint16_t* planes) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && k >= 1, "m and k must be positive (m=%lld k=%lld)", (long long)m,
+                (long long)k);
+    ENQ_REQUIRE(x && planes, "NULL pointer argument");
+    ENQ_REQUIRE(variant == ENQ_W8_FP32 || variant == ENQ_W8_BF16, "unknown variant %d", variant);
+    const int64_t kp = gemm_k_pad(k);
+    split_planes(x, nullptr, m, k, planes, m, kp, variant == ENQ_W8_FP32 ? 2 : 1);
+  });
+}
+
+extern "C" int enq_gemm_w8_planes(const uint16_t* planes, int64_t m, int64_t k,
+                                  const int8_t* codes, const float* w_scale, int64_t n,
+                                  const float* bias, int activation, float act_alpha,
+                                  float act_clip, int variant, float* y, float* z) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && n >= 1 && k >= 1, "m, n, k must be positive (m=%lld n=%lld k=%lld)",
+                (long long)m, (long long)n, (long long)k);
+    ENQ_REQUIRE(planes && codes && w_scale && y, "NULL pointer argument");
+    ENQ_REQUIRE(valid_activation(activation), "unknown activation code %d", activation);
+    ENQ_REQUIRE(variant == ENQ_W8_FP32 || variant == ENQ_W8_BF16, "unknown variant %d", variant);
+    ENQ_REQUIRE(aligned(planes, 16), "planes must be 16-byte aligned");
+    const Epilogue ep{activation, act_alpha, act_clip};
+    const int64_t kp = gemm_k_pad(k);
+    const int kmode = (k % 32 == 0 && aligned(codes, 16))
+                          ? 0
+                          : ((k % 16 == 0 && aligned(codes, 16)) ? 1 : 2);
+    auto run = [&](auto planes_tag, auto kmode_tag) {
+      gemm_dispatch<decltype(planes_tag)::value, decltype(kmode_tag)::value>(
+          planes, m * kp, kp, codes, k, w_scale, bias, m, n, k, gemm_epilogue(ep, false), y, z);
+    };
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    using K0 = std::integral_constant<int, 0>;
+    using K1 = std::integral_constant<int, 1>;
+    using K2 = std::integral_constant<int, 2>;
+    if (variant == ENQ_W8_FP32) {
+      if (kmode == 0) run(P2{}, K0{});
+      else if (kmode == 1) run(P2{}, K1{});
+      else run(P2{}, K2{});
+    } else {
+      if (kmode == 0) run(P1{}, K0{});
+      else if (kmode == 1) run(P1{}, K1{});
+      else run(P1{}, K2{});
+    }
+    finish_rows(y, m, n, ep, false);
   });
 }
 

@@ -121,6 +121,49 @@ def dense_w8(x: DeviceArray, w: Int8Weights, bias: Optional[DeviceArray] = None,
     return y
 
 
+class ActivationPlanes:
+    """Activations split once into the bf16 planes the tile kernels read
+    (``split_planes``), for several ``dense_w8_planes`` calls."""
+
+    def __init__(self, data: DeviceArray, shape: Tuple[int, ...], variant: str):
+        self.data, self.shape, self.variant = data, shape, variant
+
+
+def split_planes(x: DeviceArray, variant: str = "fp32") -> ActivationPlanes:
+    """bf16 planes of fp32 ``x`` (``..., k``): hi = bf16(x) and, for the
+    fp32-accurate variant, lo = bf16(x - hi); rows padded to a multiple of 32."""
+    if x.dtype != np.float32:
+        raise NotImplementedError(f"W8 Dense takes float32 activations, got {x.dtype}")
+    m, k = _rows(x)
+    kp = -(-k // 32) * 32
+    planes = DeviceArray((2 if variant == "fp32" else 1, m, kp), np.uint16)
+    _lib.call("enq_split_planes", x.ptr, m, k, VARIANTS[variant], planes.ptr)
+    return ActivationPlanes(planes, x.shape, variant)
+
+
+def dense_w8_planes(xp: ActivationPlanes, w: Int8Weights, bias: Optional[DeviceArray] = None,
+                    activation: str = "linear",
+                    activation_params: Optional[Dict[str, Any]] = None,
+                    out: Optional[DeviceArray] = None,
+                    pre_activation: Optional[DeviceArray] = None) -> DeviceArray:
+    """``dense_w8`` on activations already split by ``split_planes`` (the
+    tile kernels of ``dense_w8``, without the split)."""
+    k = xp.shape[-1]
+    m = int(np.prod(xp.shape[:-1], dtype=np.int64))
+    n, wk = w.shape[-2], w.shape[-1]
+    if len(w.shape) != 2:
+        raise ValueError(f"dense weights must be 2-D, got shape {w.shape}")
+    if wk != k:
+        raise ValueError(f"shapes {xp.shape} and {w.shape} not aligned: {k} (dim -1) != {wk}")
+    code, alpha, clip = activation_args(activation, activation_params)
+    y = out if out is not None else DeviceArray(xp.shape[:-1] + (n,), np.float32)
+    z = pre_activation.ptr if pre_activation is not None else null()
+    b = bias.ptr if bias is not None else null()
+    _lib.call("enq_gemm_w8_planes", xp.data.ptr, m, k, w.codes.ptr, w.scale.ptr, n, b, code,
+              alpha, clip, VARIANTS[xp.variant], y.ptr, z)
+    return y
+
+
 def dense_w8a8(x: DeviceArray, w: Int8Weights, bias: Optional[DeviceArray] = None,
                activation: str = "linear", activation_params: Optional[Dict[str, Any]] = None,
                out: Optional[DeviceArray] = None,

@@ -220,6 +220,21 @@ int enq_dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes,
                  int activation, float act_alpha, float act_clip, int variant,
                  float* y, float* z);
 
+/* The two halves of enq_dense_w8 for large m, for callers that multiply
+ * one batch of activations by several weights (the Q, K and V projections
+ * of one input): enq_split_planes writes x (m, k) fp32 as bf16 planes,
+ * hi = bf16(x) and, for ENQ_W8_FP32, lo = bf16(x - hi), each (m, kp) with kp
+ * = k rounded up to a multiple of 32 and zero padding, plane p at
+ * planes + p * m * kp (2 * planes * m * kp bytes, 16-byte aligned).
+ * enq_gemm_w8_planes then computes enq_dense_w8's y and z from them (same
+ * tile kernels as enq_dense_w8 for m > 64, no activation fake-quantization).
+ * No counterpart in the reference: they split the Dense of forward.py:318-321
+ * in two. */
+int enq_split_planes(const float* x, int64_t m, int64_t k, int variant, uint16_t* planes);
+int enq_gemm_w8_planes(const uint16_t* planes, int64_t m, int64_t k, const int8_t* codes,
+                       const float* w_scale, int64_t n, const float* bias, int activation,
+                       float act_alpha, float act_clip, int variant, float* y, float* z);
+
 /* enq_dense_w8 without any allocation.  No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same

@@ -113,6 +113,30 @@ def test_dense_w8_big_tiles(gpu, m, k, n, offset, variant, tol):
     assert np.array_equal(yh, np.maximum(zh, 0))
 
 
+@pytest.mark.parametrize("m,k,n", [(4096, 1024, 4096), (300, 784, 1024), (4100, 1040, 4100),
+                                   (129, 100, 37), (65, 48, 260)])
+@pytest.mark.parametrize("variant,tol", [("fp32", 1e-4), ("bf16", 2e-2)])
+def test_dense_w8_on_split_planes(gpu, m, k, n, variant, tol):
+    # split once, multiply twice: within the Dense bound, and for the large
+    # tiles (where dense_w8 itself splits in a separate pass) bit-identical
+    # to dense_w8
+    print(f"[case] dense_w8_planes {variant} m={m} k={k} n={n}", flush=True)
+    x, fq, codes, rows, b, wq = make(m, k, n, seed=m + 2 * k + n, wstd=0.03)
+    d_x, d_b = DeviceArray.from_numpy(x), DeviceArray.from_numpy(b)
+    xp = D.split_planes(d_x, variant)
+    for act in ("linear", "gelu"):
+        z = DeviceArray((m, n), np.float32)
+        y = D.dense_w8_planes(xp, wq, d_b, act, pre_activation=z).numpy()
+        zh = z.numpy()
+        pick = np.unique(np.concatenate([np.arange(0, m, 41), [m - 1]]))
+        z_ref = x[pick].astype(np.float64) @ fq.astype(np.float64).T + b
+        assert np.all(row_rel_err(zh[pick].astype(np.float64), z_ref) <= tol)
+        assert np.allclose(y, oracle.activate(act, zh.astype(np.float64)), rtol=2e-6, atol=2e-6)
+        if (m + 255) // 256 * ((n + 255) // 256) >= 256:
+            y2 = D.dense_w8(d_x, wq, d_b, act, variant=variant).numpy()
+            assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+
+
 @pytest.mark.parametrize("act", ["relu", "leakyrelu", "elu", "selu", "gelu", "swish", "mish",
                                  "sigmoid", "tanh", "softplus", "softmax"])
 def test_dense_w8_activations(gpu, act):
