@@ -45,17 +45,87 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float* __restrict__ y
   for (int64_t j = threadIdx.x; j < n; j += 256) row[j] = row[j] / sum;
 }
 
-__global__ __launch_bounds__(256) void act_quant_kernel(const float* __restrict__ x, int64_t n,
-                                                        Epilogue ep, float* __restrict__ y) {
+__global__ __launch_bounds__(256) void act_quant_kernel(const float* x, int64_t n, Epilogue ep,
+                                                        float* y) {
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n;
        i += int64_t(gridDim.x) * 256)
     y[i] = fake_quant(x[i], ep);
+}
+
+// 16-byte aligned x and y: workgroup b owns vectors [b * 256 * U, (b + 1) *
+// 256 * U) of 4 floats, thread t the vectors b * 256 * U + u * 256 + t.  All U
+// loads of a thread issue before its arithmetic and stores (indices clamped
+// into the array, stores masked), so a thread's requests are in flight
+// together; the last n % 4 values are done by the first threads.  x == y is
+// allowed: a thread reads its own elements before writing them.
+// fake_quant in float64 (a calibrated spec's float64 scale) with the
+// division replaced by a multiply by the reciprocal wherever that cannot
+// change the result: x * inv + zp differs from x / scale + zp by a few ulps
+// (under 1e-6 for |t| < 1e9, and larger quotients clip either way), so it
+// rounds to the same integer unless it lies within 1e-6 of a half-integer;
+// those values take the true division.  NaN and infinities fall through to
+// the same results as fake_quant.
+__device__ __forceinline__ float fake_quant_f64_recip(float v, const Epilogue& e, double inv) {
+  const double t = double(v) * inv + e.aq_zp;
+  const double fr = t - floor(t);
+  // rint keeps the sign of a zero quotient (-0.0 for small negatives)
+  const double q = fabs(fr - 0.5) < 1e-6 ? rint(double(v) / e.aq_scale + e.aq_zp) : rint(t);
+  const double c = q < double(e.aq_qmin) ? double(e.aq_qmin)
+                                          : (q > double(e.aq_qmax) ? double(e.aq_qmax) : q);
+  return float((c - e.aq_zp) * e.aq_scale);
+}
+
+template <int U, int MODE>
+__global__ __launch_bounds__(256) void act_quant_vec_kernel(const float* x, int64_t n,
+                                                            Epilogue ep, float* y) {
+  ep.aq = MODE;
+  const double inv = 1.0 / ep.aq_scale;
+  auto fq = [&](float v) {
+    if constexpr (MODE == ENQ_AQ_F64) return fake_quant_f64_recip(v, ep, inv);
+    return fake_quant(v, ep);
+  };
+  const int64_t n4 = n / 4;
+  const int64_t base = int64_t(blockIdx.x) * 256 * U + threadIdx.x;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4 v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + int64_t(u) * 256;
+    v[u] = x4[i < n4 ? i : n4 - 1];
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + int64_t(u) * 256;
+    if (i < n4) {
+      float4 r;
+      r.x = fq(v[u].x);
+      r.y = fq(v[u].y);
+      r.z = fq(v[u].z);
+      r.w = fq(v[u].w);
+      reinterpret_cast<float4*>(y)[i] = r;
+    }
+  }
+  if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+    const int64_t i = 4 * n4 + threadIdx.x;
+    y[i] = fq(x[i]);
+  }
 }
 
 }  // namespace
 
 void act_quant(const float* x, int64_t n, const Epilogue& ep, float* y) {
   if (n == 0 || ep.aq == ENQ_AQ_NONE) return;
+  if (n >= 4 && aligned(x, 16) && aligned(y, 16)) {
+    constexpr int kUnits = 4;
+    const int64_t blocks = ceil_div(n / 4, int64_t(256) * kUnits);
+    ENQ_REQUIRE(blocks <= 0x7fffffff, "tensor too large");
+    if (ep.aq == ENQ_AQ_F64)
+      act_quant_vec_kernel<kUnits, ENQ_AQ_F64><<<unsigned(blocks), 256, 0, stream()>>>(x, n, ep, y);
+    else
+      act_quant_vec_kernel<kUnits, ENQ_AQ_F32><<<unsigned(blocks), 256, 0, stream()>>>(x, n, ep, y);
+    check_launch("act_quant_vec_kernel");
+    return;
+  }
   const int64_t blocks = std::min<int64_t>(ceil_div(n, 256), int64_t(device_cu_count()) * 32);
   act_quant_kernel<<<unsigned(blocks), 256, 0, stream()>>>(x, n, ep, y);
   check_launch("act_quant_kernel");

@@ -15,6 +15,8 @@
 #include <cfloat>
 #include <cmath>
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace enq {
@@ -516,6 +518,104 @@ __global__ __launch_bounds__(kBlock) void finish_range_kernel(
       scale_from_range(b.low(), b.high(), p, scale, zp);
       scale_out[c] = scale;
       zp_out[c] = zp;
+    }
+  }
+}
+
+// Per-tensor quantize of float32 after minmax_flat_kernel, in one launch
+// with the statistics' last step.  Every workgroup first merges the `parts`
+// partial ranges itself and derives the scale and zero point from them (as
+// finish_range_kernel does; workgroup 0 also writes them out), then walks
+// its share of 4096-value chunks: each thread takes 16 consecutive values,
+// four 16-byte loads issued together, and writes its 16 codes as one 16-byte
+// store (the elementwise pass stores 4 codes per instruction).  The grid is
+// small (a few workgroups per CU), so the partials are read few times.
+// Needs 16-byte aligned x, fake and codes.
+template <bool FAKE, bool CODES, bool ERR>
+__global__ __launch_bounds__(kBlock) void quantize_flat_kernel(
+    const float* __restrict__ x, int64_t n, const PartialRange<float>* __restrict__ part,
+    int parts, QParams p, float* __restrict__ scale_out, float* __restrict__ zp_out,
+    float* __restrict__ fake, int8_t* __restrict__ codes, double* __restrict__ err_part) {
+  __shared__ float s_lo[kBlock / 64];
+  __shared__ float s_hi[kBlock / 64];
+  __shared__ int s_nan[kBlock / 64];
+  __shared__ double s_err[kBlock / 64];
+  Range<float> r;
+  r.init();
+#pragma unroll 8
+  for (int i = threadIdx.x; i < parts; i += kBlock) {
+    const PartialRange<float> e = part[i];
+    r.merge(e.lo, e.hi, e.nan);
+  }
+  wave_reduce(r);
+  if ((threadIdx.x & 63) == 0) {
+    s_lo[threadIdx.x / 64] = r.lo;
+    s_hi[threadIdx.x / 64] = r.hi;
+    s_nan[threadIdx.x / 64] = r.nan;
+  }
+  __syncthreads();
+  Range<float> b;
+  b.init();
+  for (int i = 0; i < kBlock / 64; ++i) b.merge(s_lo[i], s_hi[i], s_nan[i]);
+  float scale, zp;
+  scale_from_range(b.low(), b.high(), p, scale, zp);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    scale_out[0] = scale;
+    zp_out[0] = zp;
+  }
+  const float qmin = float(p.qmin), qmax = float(p.qmax);
+  double err = 0.0;
+  constexpr int64_t kChunk = int64_t(kBlock) * 16;
+  const int64_t chunks = ceil_div(n, kChunk);
+  for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+    const int64_t base = c * kChunk + int64_t(threadIdx.x) * 16;
+    if (base + 16 <= n) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = reinterpret_cast<const float4*>(x + base)[u];
+      uint32_t word[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float xs[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        float f[4];
+        uint32_t wd = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float q = quantize_one(xs[e], scale, zp, qmin, qmax);
+          if (CODES) wd |= uint32_t(uint8_t(code_to_i8(q))) << (8 * e);
+          if (FAKE || ERR) f[e] = dequantize_one(q, scale, zp);
+          if (ERR) {
+            const float d = f[e] - xs[e];
+            err += double(d < 0 ? -d : d);
+          }
+        }
+        word[u] = wd;
+        if (FAKE)
+          reinterpret_cast<float4*>(fake + base)[u] = make_float4(f[0], f[1], f[2], f[3]);
+      }
+      if (CODES)
+        *reinterpret_cast<uint4*>(codes + base) = make_uint4(word[0], word[1], word[2], word[3]);
+    } else {
+      for (int64_t i = base; i < n; ++i) {
+        const float q = quantize_one(x[i], scale, zp, qmin, qmax);
+        if (CODES) codes[i] = code_to_i8(q);
+        const float f = dequantize_one(q, scale, zp);
+        if (FAKE) fake[i] = f;
+        if (ERR) {
+          const float d = f - x[i];
+          err += double(d < 0 ? -d : d);
+        }
+      }
+    }
+  }
+  if (ERR) {
+    err = wave_sum(err);
+    if ((threadIdx.x & 63) == 0) s_err[threadIdx.x / 64] = err;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double total = 0.0;
+      for (int i = 0; i < kBlock / 64; ++i) total += s_err[i];
+      err_part[blockIdx.x] = total;
     }
   }
 }
@@ -1155,6 +1255,44 @@ void quantize_tensor_impl(const T* w, int64_t outer, int64_t channels, int64_t i
       check_launch("sum_doubles_kernel");
     }
     return;
+  }
+  if constexpr (std::is_same_v<T, float>) {
+    if (channels == 1 && aligned(w, 16) && (fake == nullptr || aligned(fake, 16)) &&
+        (codes == nullptr || aligned(codes, 16))) {
+      // per-tensor: the statistics pass, then one launch that finishes the
+      // statistics in every workgroup and quantizes.  8192 x 8192 to int8
+      // codes: 120-128 us as statistics, finish_range_kernel and the
+      // elementwise pass
+      const int sgrid = grid_for(ceil_div(n, 16));
+      const int qgrid = int(std::min<int64_t>(ceil_div(n, int64_t(kBlock) * 16),
+                                              int64_t(device_cu_count()) * 8));
+      const size_t part_bytes = ceil_div(sizeof(PartialRange<float>) * sgrid, 256) * 256;
+      char* ws = static_cast<char*>(workspace(part_bytes + sizeof(double) * qgrid));
+      auto* part = reinterpret_cast<PartialRange<float>*>(ws);
+      double* err_part = abs_err ? reinterpret_cast<double*>(ws + part_bytes) : nullptr;
+      minmax_flat_kernel<float, 4><<<sgrid, kBlock, 0, stream()>>>(w, n, part);
+      check_launch("minmax_flat_kernel");
+      auto launch = [&](auto fake_c, auto codes_c, auto err_c) {
+        quantize_flat_kernel<decltype(fake_c)::value, decltype(codes_c)::value,
+                             decltype(err_c)::value><<<qgrid, kBlock, 0, stream()>>>(
+            w, n, part, sgrid, p, scale, zp, fake, codes, err_part);
+      };
+      using Y = std::true_type;
+      using N = std::false_type;
+      if (fake && codes && abs_err) launch(Y{}, Y{}, Y{});
+      else if (fake && codes) launch(Y{}, Y{}, N{});
+      else if (fake && abs_err) launch(Y{}, N{}, Y{});
+      else if (codes && abs_err) launch(N{}, Y{}, Y{});
+      else if (fake) launch(Y{}, N{}, N{});
+      else if (codes) launch(N{}, Y{}, N{});
+      else launch(N{}, N{}, Y{});
+      check_launch("quantize_flat_kernel");
+      if (abs_err) {
+        sum_doubles_kernel<<<1, kBlock, 0, stream()>>>(err_part, qgrid, abs_err);
+        check_launch("sum_doubles_kernel");
+      }
+      return;
+    }
   }
   range_stats<T>(w, outer, channels, inner, p, true, nullptr, nullptr, scale, zp);
   const int grid = elementwise_grid<T>(n);

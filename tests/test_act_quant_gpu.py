@@ -52,6 +52,22 @@ def test_standalone_pass_bit_exact(gpu, dtype, scheme, bits):
     assert np.array_equal(got[~nan].view(np.uint32), w32[~nan].view(np.uint32))
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 1023, 4096 * 1024 + 2])
+@pytest.mark.parametrize("in_place", [False, True])
+def test_standalone_pass_sizes(gpu, n, in_place):
+    # the vector kernel (16-byte aligned, n >= 4) with its n % 4 tail, and
+    # the scalar kernel below 4 values; in place as Forward applies it
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 2).astype(np.float32)
+    for spec_dtype in (np.float64, np.float32):
+        spec = spec_for(x if n > 1 else np.array([-1.0, 1.0]), 8, "asymmetric", spec_dtype)
+        want = oracle.fake_quantize(x, spec["scale"], spec["zero_point"], 8,
+                                    "asymmetric").astype(np.float32)
+        d_x = DeviceArray.from_numpy(x)
+        got = D.act_quant(d_x, spec, out=d_x if in_place else None).numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("scale", [0.1, 0.02, 1.0 / 3.0, 0.0234375, 3.7, 1e-3])
 @pytest.mark.parametrize("zp", [0.0, 3.0, 117.0])
 def test_standalone_pass_rounding_ties(gpu, scale, zp):
