@@ -100,6 +100,10 @@ SIGNATURES = {
     "enq_dense_w8_aq": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, _P, c_int, c_float,
                                 c_float, c_int, c_int, c_double, c_double, c_float, c_float,
                                 _P, _P]),
+    "enq_dense_w8a8_static": (c_int, [_P, c_int64, c_int64, c_int, c_double, c_double, c_float,
+                                      c_float, _P, _P, _P, c_int64, _P, c_int, c_float, c_float,
+                                      _P, _P]),
+    "enq_code_row_sums": (c_int, [_P, c_int64, c_int64, _P]),
     "enq_act_quant": (c_int, [_P, c_int64, c_int, c_double, c_double, c_float, c_float, _P]),
     "enq_layernorm": (c_int, [_P, c_int64, c_int64, _P, _P, c_float, _P]),
     "enq_add": (c_int, [_P, _P, c_int64, _P]),

@@ -9,6 +9,10 @@
 //   (acc.astype(float32) * x_scale) * w_scale.T + b.
 #pragma clang fp contract(off)
 
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+
 #include "common.hpp"
 #include "epilogue.hpp"
 #include "mfma.hpp"
@@ -48,7 +52,8 @@ __global__ __launch_bounds__(WM * WN * 64) void w8a8_gemm_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ x_scale,
     const int8_t* __restrict__ wq, const float* __restrict__ w_scale,
     const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_n, Epilogue ep,
-    float* __restrict__ y, int32_t* __restrict__ acc_out) {
+    float* __restrict__ y, int32_t* __restrict__ acc_out, const int32_t* __restrict__ w_sums,
+    int corr) {
   constexpr int NT = WM * WN * 64;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
@@ -152,13 +157,14 @@ __global__ __launch_bounds__(WM * WN * 64) void w8a8_gemm_kernel(
     if (col >= n) continue;
     const float sw = w_scale[col];
     const float b = bias ? bias[col] : 0.f;
+    const int32_t add = w_sums ? corr * w_sums[col] : 0;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
         if (row < m) {
-          const int32_t a = acc[i][j][e];
+          const int32_t a = acc[i][j][e] + add;
           if (acc_out) acc_out[row * n + col] = a;
           float v = float(a) * x_scale[row];
           v = v * sw;
@@ -197,7 +203,8 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ x_scale,
     const int8_t* __restrict__ wq, const float* __restrict__ w_scale,
     const float* __restrict__ bias, int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n,
-    Epilogue ep, float* __restrict__ y, int32_t* __restrict__ acc_out) {
+    Epilogue ep, float* __restrict__ y, int32_t* __restrict__ acc_out,
+    const int32_t* __restrict__ w_sums, int corr) {
   constexpr int BM = R::BM, BN = R::BN, BK = R::BK, STAGES = R::STAGES;
   constexpr int WN = R::WN, TM = R::TM, TN = R::TN, FM = R::FM, FN = R::FN;
   constexpr int STAGE_BYTES = R::STAGE_BYTES, DMA_PER_WAVE = R::DMA_PER_WAVE;
@@ -303,12 +310,14 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
   // that they arrive during the main loop; being older than every DMA they
   // only make the stage waits conservative
   float sw[FN], bj[FN];
+  int32_t add[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     int64_t col = n0 + wn * TN + j * 32 + lrow;
     col = col < n ? col : n - 1;
     sw[j] = w_scale[col];
     bj[j] = bias ? bias[col] : 0.f;
+    add[j] = w_sums ? corr * w_sums[col] : 0;
   }
   // Stage t is complete for every wave once this wave's own DMA for it has
   // landed (vmcnt counts the later stages still in flight) and all waves
@@ -390,7 +399,7 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
         for (int e = 0; e < 16; ++e) {
           const int64_t row = row0 + 8 * (e / 4) + (e % 4);
           if (row < m) {
-            const int32_t a = acc[i][j][e];
+            const int32_t a = acc[i][j][e] + add[j];
             if (acc_out) acc_out[row * n + col] = a;
             float v = float(a) * xs[e];
             v = v * sw[j];
@@ -406,7 +415,7 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
 template <class R>
 void launch_w8a8_ring(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws,
                       const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep,
-                      float* y, int32_t* acc) {
+                      float* y, int32_t* acc, const int32_t* w_sums, int corr) {
   const int64_t tiles_m = ceil_div(m, R::BM), tiles_n = ceil_div(n, R::BN);
   ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
   const size_t lds_bytes = size_t(R::STAGES) * R::STAGE_BYTES;
@@ -420,14 +429,14 @@ void launch_w8a8_ring(const int8_t* xq, const float* xs, const int8_t* wq, const
   }
   auto kernel = (k % R::BK == 0) ? w8a8_ring_kernel<R, false> : w8a8_ring_kernel<R, true>;
   kernel<<<unsigned(tiles_m * tiles_n), R::NT, lds_bytes, stream()>>>(
-      xq, xs, wq, ws, bias, m, n, k, int(tiles_m), int(tiles_n), ep, y, acc);
+      xq, xs, wq, ws, bias, m, n, k, int(tiles_m), int(tiles_n), ep, y, acc, w_sums, corr);
   check_launch("w8a8_ring_kernel");
 }
 
 template <int BM, int BN, int WM, int WN, int KMODE>
 void launch_w8a8(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws,
                  const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep, float* y,
-                 int32_t* acc) {
+                 int32_t* acc, const int32_t* w_sums, int corr) {
   const int64_t tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
   ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
   const size_t lds_bytes = size_t(2) * (BM + BN) * kPitch8;
@@ -439,39 +448,92 @@ void launch_w8a8(const int8_t* xq, const float* xs, const int8_t* wq, const floa
     attr_set = true;
   }
   kernel<<<unsigned(tiles_m * tiles_n), WM * WN * 64, lds_bytes, stream()>>>(
-      xq, xs, wq, ws, bias, m, n, k, int(tiles_n), ep, y, acc);
+      xq, xs, wq, ws, bias, m, n, k, int(tiles_n), ep, y, acc, w_sums, corr);
   check_launch("w8a8_gemm_kernel");
 }
 
 template <int KMODE>
 void w8a8_dispatch(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws,
                    const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep,
-                   float* y, int32_t* acc) {
+                   float* y, int32_t* acc, const int32_t* w_sums, int corr) {
   const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256);
   if (big_tiles >= device_cu_count())
-    launch_w8a8<256, 256, 4, 2, KMODE>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+    launch_w8a8<256, 256, 4, 2, KMODE>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc, w_sums, corr);
   else
-    launch_w8a8<128, 128, 2, 2, KMODE>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+    launch_w8a8<128, 128, 2, 2, KMODE>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc, w_sums, corr);
 }
 
 }  // namespace
 
+// w_sums (nullable): per output row of wq, the sum of its codes; corr * w_sums[n]
+// is added to every accumulator of column n (exact int32), which turns codes
+// stored shifted by `shift` with a zero point zp (corr = shift - zp) back into
+// sum_k (q - zp) w.
 void gemm_w8a8(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws,
                const float* bias, int64_t m, int64_t n, int64_t k, const Epilogue& ep, float* y,
-               int32_t* acc) {
+               int32_t* acc, const int32_t* w_sums = nullptr, int corr = 0) {
   const bool al = aligned(xq, 16) && aligned(wq, 16);
   const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256);
   if (k % 16 == 0 && al && big_tiles >= device_cu_count() / 2) {
-    launch_w8a8_ring<W8a8Ring>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+    launch_w8a8_ring<W8a8Ring>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc, w_sums, corr);
   }
   else if (k % kBK8 == 0 && al)
-    w8a8_dispatch<0>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+    w8a8_dispatch<0>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc, w_sums, corr);
   else if (k % 16 == 0 && al)
-    w8a8_dispatch<1>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+    w8a8_dispatch<1>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc, w_sums, corr);
   else
-    w8a8_dispatch<2>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc);
+    w8a8_dispatch<2>(xq, xs, wq, ws, bias, m, n, k, ep, y, acc, w_sums, corr);
   finish_rows(y, m, n, ep, false);
 }
+
+namespace {
+
+// Codes of x under a calibrated per-tensor spec (forward.py:798-805 with
+// quantize, quantization.py:53-56): q = clip(rint(x / scale + zp), qmin,
+// qmax) in the spec's arithmetic (float64 or float32), stored as int8 q -
+// shift; every row's x_scale is float(scale).
+__global__ __launch_bounds__(256) void quantize_static_kernel(
+    const float* __restrict__ x, int64_t n, int64_t rows, Epilogue ep, int shift,
+    int8_t* __restrict__ codes, float* __restrict__ x_scale) {
+  const double inv = 1.0 / ep.aq_scale;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * 256) {
+    const float v = x[i];
+    double q;
+    if (ep.aq == ENQ_AQ_F64) {
+      // multiply by the reciprocal except within 1e-6 of a rounding tie,
+      // where the two can differ: then the true division
+      const double t = double(v) * inv + ep.aq_zp;
+      const double fr = t - floor(t);
+      q = fabs(fr - 0.5) < 1e-6 ? rint(double(v) / ep.aq_scale + ep.aq_zp) : rint(t);
+    } else {
+      q = double(rintf(__fdiv_rn(v, float(ep.aq_scale)) + float(ep.aq_zp)));
+    }
+    // NaN stays NaN through the reference's clip; its code is 0 (q = shift)
+    q = q != q ? double(shift) : (q < double(ep.aq_qmin) ? double(ep.aq_qmin)
+                                  : (q > double(ep.aq_qmax) ? double(ep.aq_qmax) : q));
+    codes[i] = int8_t(int(q) - shift);
+  }
+  for (int64_t r = int64_t(blockIdx.x) * 256 + threadIdx.x; r < rows;
+       r += int64_t(gridDim.x) * 256)
+    x_scale[r] = float(ep.aq_scale);
+}
+
+// sums[r] = sum of the k int8 codes of row r (one wave per row).
+__global__ __launch_bounds__(256) void code_row_sums_kernel(const int8_t* __restrict__ codes,
+                                                            int64_t rows, int64_t k,
+                                                            int32_t* __restrict__ sums) {
+  const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const int8_t* row = codes + r * k;
+  int32_t s = 0;
+  for (int64_t i = lane; i < k; i += 64) s += row[i];
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) sums[r] = s;
+}
+
+}  // namespace
 
 }  // namespace enq
 
@@ -491,6 +553,67 @@ int enq_gemm_w8a8(const int8_t* x_codes, const float* x_scale, const int8_t* w_c
     ENQ_REQUIRE(valid_activation(activation), "unknown activation code %d", activation);
     Epilogue ep{activation, act_alpha, act_clip};
     gemm_w8a8(x_codes, x_scale, w_codes, w_scale, bias, m, n, k, ep, y, acc);
+  });
+}
+
+int enq_code_row_sums(const int8_t* codes, int64_t rows, int64_t k, int32_t* sums) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(rows >= 1 && k >= 1, "rows and k must be positive");
+    ENQ_REQUIRE(k <= 16909320, "k=%lld can overflow an int32 code sum", (long long)k);
+    ENQ_REQUIRE(codes && sums, "NULL pointer argument");
+    const int64_t blocks = ceil_div(rows, 4);
+    ENQ_REQUIRE(blocks <= 0x7fffffff, "too many rows");
+    code_row_sums_kernel<<<unsigned(blocks), 256, 0, stream()>>>(codes, rows, k, sums);
+    check_launch("code_row_sums_kernel");
+  });
+}
+
+int enq_dense_w8a8_static(const float* x, int64_t m, int64_t k, int aq_mode, double x_scale,
+                          double x_zero_point, float qmin, float qmax, const int8_t* codes,
+                          const float* w_scale, const int32_t* w_code_sums, int64_t n,
+                          const float* bias, int activation, float act_alpha, float act_clip,
+                          float* y, int32_t* acc) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && n >= 1 && k >= 1, "m, n, k must be positive");
+    ENQ_REQUIRE(x && codes && w_scale && y, "NULL pointer argument");
+    ENQ_REQUIRE(valid_activation(activation), "unknown activation code %d", activation);
+    ENQ_REQUIRE(aq_mode == ENQ_AQ_F32 || aq_mode == ENQ_AQ_F64, "unknown act-quant mode %d",
+                aq_mode);
+    ENQ_REQUIRE(valid_act_quant(aq_mode, x_scale, qmin, qmax), "invalid act-quant parameters");
+    ENQ_REQUIRE(qmin == float(int(qmin)) && qmax == float(int(qmax)) && qmax - qmin <= 255.0f,
+                "the activation grid [%g, %g] does not fit 8 bits", double(qmin), double(qmax));
+    ENQ_REQUIRE(x_zero_point == double(int64_t(x_zero_point)) && x_zero_point >= -1024 &&
+                    x_zero_point <= 1024,
+                "the zero point must be a small integer (got %g)", x_zero_point);
+    // codes are stored as int8 q - shift
+    const int shift = qmax > 127.0f ? 128 : 0;
+    ENQ_REQUIRE(qmin - shift >= -128.0f && qmax - shift <= 127.0f,
+                "the activation grid [%g, %g] does not fit int8", double(qmin), double(qmax));
+    const int corr = shift - int(x_zero_point);
+    ENQ_REQUIRE(corr == 0 || w_code_sums, "w_code_sums is needed for a zero point of %g",
+                x_zero_point);
+    // |sum (q - shift) w| + |corr sum w| <= (128 + |corr|) * 127 * k < 2^31
+    ENQ_REQUIRE(double(128 + std::abs(corr)) * 127.0 * double(k) < 2147483648.0,
+                "k=%lld can overflow the int32 accumulator", (long long)k);
+    const size_t code_bytes = (size_t(m) * size_t(k) + 255) / 256 * 256;
+    char* ws = static_cast<char*>(workspace(code_bytes + sizeof(float) * size_t(m)));
+    auto* xq = reinterpret_cast<int8_t*>(ws);
+    auto* xs = reinterpret_cast<float*>(ws + code_bytes);
+    Epilogue aq{ENQ_ACT_LINEAR, 0.f, 0.f};
+    aq.aq = aq_mode;
+    aq.aq_scale = x_scale;
+    aq.aq_zp = x_zero_point;
+    aq.aq_qmin = qmin;
+    aq.aq_qmax = qmax;
+    const int64_t total = m * k;
+    const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), int64_t(device_cu_count()) * 32);
+    quantize_static_kernel<<<unsigned(blocks), 256, 0, stream()>>>(x, total, m, aq, shift, xq, xs);
+    check_launch("quantize_static_kernel");
+    Epilogue ep{activation, act_alpha, act_clip};
+    gemm_w8a8(xq, xs, codes, w_scale, bias, m, n, k, ep, y, acc, corr ? w_code_sums : nullptr,
+              corr);
   });
 }
 

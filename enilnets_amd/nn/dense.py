@@ -167,9 +167,14 @@ def dense_w8_planes(xp: ActivationPlanes, w: Int8Weights, bias: Optional[DeviceA
 def dense_w8a8(x: DeviceArray, w: Int8Weights, bias: Optional[DeviceArray] = None,
                activation: str = "linear", activation_params: Optional[Dict[str, Any]] = None,
                out: Optional[DeviceArray] = None,
-               acc: Optional[DeviceArray] = None) -> DeviceArray:
-    """Per-token int8 activation codes times int8 weights, int32
-    accumulation (``acc`` receives the accumulators when given)."""
+               acc: Optional[DeviceArray] = None,
+               x_spec: Optional[Dict[str, Any]] = None,
+               x_dtype: Any = np.float32) -> DeviceArray:
+    """int8 activation codes times int8 weights, int32 accumulation (``acc``
+    receives the accumulators when given).  The activations are quantized
+    per token (symmetric, dynamic), or with ``x_spec`` -- the calibrated
+    ``act_quant`` spec of the layer that produced ``x``, whose host dtype is
+    ``x_dtype`` -- per tensor on that spec's grid (static W8A8)."""
     if x.dtype != np.float32:
         raise NotImplementedError(f"W8A8 Dense takes float32 activations, got {x.dtype}")
     m, k = _rows(x)
@@ -178,9 +183,18 @@ def dense_w8a8(x: DeviceArray, w: Int8Weights, bias: Optional[DeviceArray] = Non
         raise ValueError(f"shapes {x.shape} and {w.shape} not aligned: {k} (dim -1) != {wk}")
     code, alpha, clip = activation_args(activation, activation_params)
     y = out if out is not None else DeviceArray(x.shape[:-1] + (n,), np.float32)
-    _lib.call("enq_dense_w8a8", x.ptr, m, k, w.codes.ptr, w.scale.ptr, n,
-              bias.ptr if bias is not None else null(), code, alpha, clip, y.ptr,
-              acc.ptr if acc is not None else null())
+    b = bias.ptr if bias is not None else null()
+    a = acc.ptr if acc is not None else null()
+    if x_spec is None:
+        _lib.call("enq_dense_w8a8", x.ptr, m, k, w.codes.ptr, w.scale.ptr, n, b, code, alpha,
+                  clip, y.ptr, a)
+        return y
+    mode, scale, zp, qmin, qmax, _ = act_quant_args(x_spec, x_dtype)
+    # the zero-point term needs the weight's code sums unless it vanishes
+    shift = 128 if qmax > 127 else 0
+    sums = w.code_sums.ptr if shift != zp else null()
+    _lib.call("enq_dense_w8a8_static", x.ptr, m, k, mode, scale, zp, qmin, qmax, w.codes.ptr,
+              w.scale.ptr, sums, n, b, code, alpha, clip, y.ptr, a)
     return y
 
 

@@ -42,7 +42,7 @@ class Int8Weights:
     fp32 scale per output row, resident on the device."""
 
     __slots__ = ("codes", "scale", "shape", "bits", "per_channel", "source_id",
-                 "source_digest")
+                 "source_digest", "_code_sums")
 
     def __init__(self, codes: DeviceArray, scale: DeviceArray, shape, bits: int,
                  per_channel: bool, source: Optional[np.ndarray], scale_host: Any):
@@ -54,6 +54,18 @@ class Int8Weights:
         self.source_id = id(source) if source is not None else None
         self.source_digest = (_digest(source) ^ _digest(np.asarray(scale_host, np.float32))
                               if source is not None else None)
+        self._code_sums = None
+
+    @property
+    def code_sums(self) -> DeviceArray:
+        """Per output row, the sum of its int8 codes (int32, device), made
+        once: the zero-point term of static W8A8."""
+        if self._code_sums is None:
+            rows, k = self.shape[-2], self.shape[-1]
+            sums = DeviceArray((rows,), np.int32)
+            _lib.call("enq_code_row_sums", self.codes.ptr, rows, k, sums.ptr)
+            self._code_sums = sums
+        return self._code_sums
 
     def __deepcopy__(self, memo):
         return None

@@ -290,6 +290,29 @@ int enq_dense_w8a8(const float* x, int64_t m, int64_t k, const int8_t* codes,
                    int activation, float act_alpha, float act_clip, float* y,
                    int32_t* acc);
 
+/* Static W8A8 Dense: the activations are quantized with a calibrated
+ * per-tensor spec (ActivationCalibrator, quantization.py:156-209: the
+ * act_quant spec of the layer that produced x, applied as forward.py:798-805
+ * does) instead of per token.  Codes q = clip(rint(x / x_scale +
+ * x_zero_point), qmin, qmax) in the spec's arithmetic (aq_mode ENQ_AQ_F32 or
+ * ENQ_AQ_F64), so for an x the spec already fake-quantized they are that
+ * grid's integers exactly.  acc[m,n] = sum_k (q - zp) * codes[n,k] (exact
+ * int32), y = act((float(acc) * float(x_scale)) * w_scale[n] + bias[n]).
+ * Grids wider than int8 (asymmetric [0, 255]) are stored shifted by 128, and
+ * (128 - zp) * w_code_sums[n] is added back to the accumulators:
+ * w_code_sums (from enq_code_row_sums) may be NULL only when that term is 0.
+ * No counterpart in the reference (it has no integer GEMM); the composed
+ * oracle is its quantize (:53-56) and Dense (forward.py:318-321). */
+int enq_dense_w8a8_static(const float* x, int64_t m, int64_t k, int aq_mode,
+                          double x_scale, double x_zero_point, float qmin, float qmax,
+                          const int8_t* codes, const float* w_scale,
+                          const int32_t* w_code_sums, int64_t n, const float* bias,
+                          int activation, float act_alpha, float act_clip, float* y,
+                          int32_t* acc);
+
+/* sums[r] = sum over k of codes[r, k] (int32), for enq_dense_w8a8_static. */
+int enq_code_row_sums(const int8_t* codes, int64_t rows, int64_t k, int32_t* sums);
+
 /* ---- Transformer-block pieces around the quantized projections -------
  * LayerNorm over the last axis of an fp32 (rows, cols) matrix:
  * y = gamma * (x - mean) / sqrt(var + eps) + beta, mean and biased variance

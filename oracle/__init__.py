@@ -20,13 +20,14 @@ from .quantization import (QUANTIZABLE, compute_scale, dequantize,
 from .qat import MovingRange, qat_linear_forward, qat_quantized_weight, ste_mask
 from .calibration import observe_ranges, percentile, specs_from_ranges
 from .forward import (activate, dense_forward, forward, forward_top_k, layernorm_forward,
-                      mha_forward, moe_forward, router, top_k, w8a8_dense, window_mask)
+                      mha_forward, moe_forward, router, top_k, w8a8_dense, w8a8_static_dense,
+                      window_mask)
 
 __all__ = [
     "QUANTIZABLE", "compute_scale", "dequantize", "fake_quantize",
     "quant_range", "quantization_error", "quantize", "quantize_tensor",
     "quantize_weights", "int8_codes", "activate", "dense_forward", "forward",
-    "layernorm_forward", "mha_forward", "moe_forward", "w8a8_dense", "forward_top_k",
+    "layernorm_forward", "mha_forward", "moe_forward", "w8a8_dense", "w8a8_static_dense", "forward_top_k",
     "router", "top_k", "window_mask", "MovingRange", "qat_linear_forward",
     "qat_quantized_weight", "ste_mask", "observe_ranges", "percentile", "specs_from_ranges",
 ]

@@ -206,6 +206,33 @@ def w8a8_dense(x: Any, w_codes: np.ndarray, w_scale: Any, bias: Any = None,
     return activate(activation, y), acc, x_scale, x_codes
 
 
+def w8a8_static_dense(x: Any, spec: Dict[str, Any], w_codes: np.ndarray, w_scale: Any,
+                      bias: Any = None, activation: str = "linear") -> Tuple[Any, np.ndarray, Any]:
+    """Composed static W8A8 Dense: ``(y, acc_int32, x_codes)``.
+
+    The activations take the calibrated per-tensor spec of the layer that
+    produced them (``ActivationCalibrator``, ``compression/quantization.py:
+    156-209``): ``q = quantize(x, scale, zero_point, bits, scheme)``
+    (``:53-56``) in the dtype NumPy gives it; ``acc`` is the exact integer
+    sum of ``(q - zero_point) * w_codes`` and ``y = act((acc * scale) *
+    w_scale + b)`` in float32, evaluated in that order; for an ``x`` already
+    fake-quantized by the spec, ``acc * scale * w_scale`` is the reference's
+    ``x @ W.T`` (``nn/forward.py:318-319``) up to float rounding."""
+    q = quantize(np.asarray(x, dtype=np.float32), spec["scale"], spec["zero_point"],
+                 spec["bits"], spec["scheme"])
+    zp = float(np.asarray(spec["zero_point"]).reshape(-1)[0])
+    centred = q.astype(np.float64) - zp
+    acc = np.dot(centred, w_codes.astype(np.float64).T).astype(np.int64)
+    assert np.all(np.abs(acc) < 2 ** 31)
+    acc = acc.astype(np.int32)
+    ws = np.asarray(w_scale, dtype=np.float32).reshape(1, -1)
+    s32 = np.float32(np.asarray(spec["scale"]).reshape(-1)[0])
+    y = (acc.astype(np.float32) * s32) * ws
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=np.float32)
+    return activate(activation, y), acc, q
+
+
 def forward(layers: List[Dict[str, Any]], inputs: Any,
             dtype: Any = np.float32) -> List[Any]:
     """Run the layer list; returns every layer's output (``outputs[0]`` is

@@ -221,3 +221,37 @@ def test_w8a8_square_8192(gpu):
     # a checksum of all rows: sum over n of acc equals x . (sum of W rows)
     wsum = wc.astype(np.int64).sum(axis=0)
     assert np.array_equal(got.astype(np.int64).sum(axis=1), xc.astype(np.int64) @ wsum)
+
+
+STATIC_SPECS = [("asymmetric", 8, np.float64), ("symmetric", 8, np.float32),
+                ("asymmetric", 4, np.float64), ("symmetric", 8, np.float64)]
+
+
+@pytest.mark.parametrize("m,k,n", [(64, 512, 300), (4096, 1024, 4096), (300, 1000, 70),
+                                   (200, 1040, 2100)])
+@pytest.mark.parametrize("spec_i", range(len(STATIC_SPECS)))
+def test_w8a8_static(gpu, m, k, n, spec_i):
+    # activations quantized with a calibrated per-tensor spec: int32
+    # accumulators and the linear output bit-identical to the composed
+    # oracle; on activations the spec already fake-quantized, within the
+    # Dense bound of the reference's float Dense of those values
+    scheme, bits, sdt = STATIC_SPECS[spec_i]
+    print(f"[case] w8a8 static {scheme}{bits} {np.dtype(sdt).name} m={m} k={k} n={n}", flush=True)
+    x, fq, codes, rows, b, wq = make(m, k, n, seed=m + k + n + spec_i)
+    x = x * 1.5 + 0.25
+    low, high = float(x.min()), float(x.max())
+    scale, zp = oracle.compute_scale(np.asarray(low, sdt), np.asarray(high, sdt), bits, scheme)
+    spec = {"bits": bits, "scheme": scheme, "scale": scale, "zero_point": zp}
+    x_fq = oracle.fake_quantize(x, scale, zp, bits, scheme).astype(np.float32)
+    for xin in (x_fq, x):
+        acc = DeviceArray((m, n), np.int32)
+        y = D.dense_w8a8(DeviceArray.from_numpy(xin), wq, DeviceArray.from_numpy(b), "linear",
+                         acc=acc, x_spec=spec).numpy()
+        y_ref, acc_ref, _ = oracle.w8a8_static_dense(xin, spec, codes, rows, b)
+        assert np.array_equal(acc.numpy(), acc_ref)
+        assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
+    z_ref = x_fq.astype(np.float64) @ fq.astype(np.float64).T + b
+    y = D.dense_w8a8(DeviceArray.from_numpy(x_fq), wq, DeviceArray.from_numpy(b), "relu",
+                     x_spec=spec).numpy()
+    err = np.max(np.abs(y - np.maximum(z_ref, 0)), axis=1) / np.max(np.abs(z_ref), axis=1)
+    assert np.all(err <= 1e-4), f"max row error {err.max():.3e}"

@@ -691,3 +691,36 @@ def test_observe_ranges_and_specs():
     assert float(specs[2]["scale"]) == float(np.float64(high - low) / 255)
     with pytest.raises(RuntimeError):
         oracle.specs_from_ranges({})
+
+
+def test_w8a8_static_accumulator_and_grid_identity():
+    # static W8A8 (calibrated per-tensor activation spec): the accumulator is
+    # the exact integer dot product of (q - zp) and the weight codes, and for
+    # activations already on the spec's grid, acc * scale * w_scale is the
+    # float Dense of the fake-quantized values
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal((7, 33)).astype(np.float32) * 2
+    low, high = float(x.min()), float(x.max())
+    scale, zp = oracle.compute_scale(np.asarray(low), np.asarray(high), 8, "asymmetric")
+    spec = {"bits": 8, "scheme": "asymmetric", "scale": scale, "zero_point": zp}
+    assert float(zp) != 0.0
+    x_fq = oracle.fake_quantize(x, scale, zp, 8, "asymmetric").astype(np.float32)
+    w = (rng.standard_normal((5, 33)) * 0.1).astype(np.float32)
+    w_codes, w_scale = oracle.int8_codes(w, per_channel=True)
+    y, acc, q = oracle.w8a8_static_dense(x_fq, spec, w_codes, w_scale.reshape(-1))
+    zi = int(zp)
+    exact = [[sum((int(q[i, k]) - zi) * int(w_codes[j, k]) for k in range(33)) for j in range(5)]
+             for i in range(7)]
+    assert np.array_equal(acc, np.array(exact, np.int32))
+    fq_w = w_codes.astype(np.float64) * w_scale.astype(np.float64).reshape(-1, 1)
+    # the grid values themselves, (q - zp) * scale in float64
+    grid = (q.astype(np.float64) - float(zp)) * float(scale)
+    want = grid @ fq_w.T
+    got = acc * float(scale) * w_scale.astype(np.float64).reshape(1, -1)
+    assert np.max(np.abs(got - want)) <= 1e-12 * np.abs(want).max()
+    # the float32 fake-quantized activations differ from the grid by their rounding
+    want32 = x_fq.astype(np.float64) @ fq_w.T
+    assert np.max(np.abs(y - want32)) <= 1e-5 * np.abs(want32).max()
+    # planted mistake: the zero point left out of the accumulator
+    bad = np.dot(q.astype(np.float64), w_codes.astype(np.float64).T)
+    assert not np.array_equal(bad.astype(np.int64), acc.astype(np.int64))
