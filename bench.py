@@ -466,7 +466,7 @@ def next_rows(timer, rng):
 
     # QAT forward: per-step per-channel weight fake-quantization feeding the
     # W8 Dense (QATLinear.forward, training=False)
-    q = QATLinear(w, np.zeros(N, np.float32))
+    q = QATLinear.from_weights(w, np.zeros(N, np.float32))
     q.forward(x, training=False)
     ms = timer.time(lambda i: q.forward(x, training=False), 20)
     out["qat_forward_4096x1024x1024"] = {

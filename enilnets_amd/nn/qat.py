@@ -52,17 +52,36 @@ class MovingRangeObserver:
 
 class QATLinear:
     """Device twin of ``graph.quantization.QATLinear`` (``:94-141``) for the
-    forward pass: weight ``(n_out, n_in)`` float32, bias ``(n_out,)``."""
+    forward pass.  ``QATLinear(n_in, n_out, ...)`` takes the reference's
+    arguments (``:106-117``: ``init_weights(n_in, n_out, init_method)``, a
+    ``(n_out, n_in)`` weight and zero bias); ``QATLinear.from_weights``
+    starts from given float32 arrays."""
 
-    def __init__(self, weight: Any, bias: Any = None, bits: int = 8, per_channel: bool = True,
-                 quantize_activations: bool = False, act_bits: int = 8) -> None:
-        w = np.ascontiguousarray(weight, dtype=np.float32)
+    def __init__(self, n_in: int, n_out: int, bits: int = 8, per_channel: bool = True,
+                 quantize_activations: bool = False, act_bits: int = 8,
+                 init_method: str = "xavier_uniform") -> None:
+        from .weight_init import init_weights
+        w, b = init_weights(int(n_in), int(n_out), method=init_method)
+        self._setup(w, b, bits, per_channel, quantize_activations, act_bits)
+
+    @classmethod
+    def from_weights(cls, weight: Any, bias: Any = None, bits: int = 8, per_channel: bool = True,
+                     quantize_activations: bool = False, act_bits: int = 8) -> "QATLinear":
+        """A layer with weight ``(n_out, n_in)`` and bias ``(n_out,)`` (zero when None)."""
+        self = cls.__new__(cls)
+        w = np.asarray(weight, dtype=np.float32)
         if w.ndim != 2:
             raise ValueError(f"QATLinear weight must be 2-D, got {w.shape}")
+        b = np.zeros(w.shape[0], np.float32) if bias is None else bias
+        self._setup(w, b, bits, per_channel, quantize_activations, act_bits)
+        return self
+
+    def _setup(self, w: np.ndarray, b: Any, bits: int, per_channel: bool,
+               quantize_activations: bool, act_bits: int) -> None:
+        w = np.ascontiguousarray(w, dtype=np.float32)
         if not 2 <= int(bits) <= 8:
             raise NotImplementedError("the device QAT forward takes 2- to 8-bit weights")
         self.weight = DeviceArray.from_numpy(w)
-        b = np.zeros(w.shape[0], np.float32) if bias is None else bias
         self.bias = DeviceArray.from_numpy(np.ascontiguousarray(b, dtype=np.float32))
         self.bits, self.act_bits = int(bits), int(act_bits)
         self.per_channel = per_channel

@@ -150,3 +150,29 @@ def test_int8_file_rejects_other_archives(tmp_path):
         np.savez(fh, meta=meta)
     with pytest.raises(ValueError):
         LoadInt8(str(f))
+
+
+def test_init_weights_layout_and_methods():
+    # nn/weight_init.py:11-46: weights (n_out, n_in) float32, zero bias, the
+    # method's bounds; orthogonal rows orthonormal; unknown names raise
+    from enilnets_amd.nn.weight_init import init_weights
+    np.random.seed(3)
+    for method in ("xavier_uniform", "xavier_normal", "he_uniform", "he_normal", "normal",
+                   "orthogonal", "zeros", "ones"):
+        w, b = init_weights(40, 24, method=method)
+        assert w.shape == (24, 40) and w.dtype == np.float32
+        assert b.shape == (24,) and not b.any()
+    w, _ = init_weights(40, 24, "xavier_uniform")
+    assert np.abs(w).max() <= np.sqrt(6 / 64) and np.abs(w).max() > 0.5 * np.sqrt(6 / 64)
+    w, _ = init_weights(40, 24, "he_uniform")
+    assert np.abs(w).max() <= np.sqrt(6 / 40)
+    w, _ = init_weights(40, 24, "orthogonal")
+    assert np.allclose(w @ w.T, np.eye(24), atol=1e-5)
+    # a seeded run draws the same weights twice
+    np.random.seed(11)
+    w1, _ = init_weights(7, 5, "he_normal")
+    np.random.seed(11)
+    w2, _ = init_weights(7, 5, "he_normal")
+    assert np.array_equal(w1, w2)
+    with pytest.raises(ValueError):
+        init_weights(4, 4, "nope")
