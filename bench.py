@@ -6,8 +6,9 @@
 Headline (``value``): BASELINE.json configs[2], the largest single-GPU
 configuration: the W8 Dense of an 8192 x 8192 weight (N(0, 0.02), quantized
 per output channel to int8) on M = 4096 fp32 activations (N(0, 1)), on the
-fp32-accurate path (bf16 hi + lo activation planes on the matrix cores, fp32
-accumulation).  One step is one Dense call over that batch, inputs resident
+fp32-accurate path (per row a power-of-two scale, fp16 high parts and e4m3
+low parts of the activations on the fp16 and fp8 matrix cores, one fp32
+accumulator).  One step is one Dense call over that batch, inputs resident
 in HBM; the metric is the algorithmic TFLOP/s, 2 * M * N * K per step.
 
 ``components`` reports the other configs[2] kernels (quantize / dequantize
@@ -39,7 +40,7 @@ INT8_PEAK_TOPS = 5000.0        # dense int8 MFMA
 FP32_PEAK_TFLOPS = 157.3       # fp32 MFMA
 
 
-def measured_traffic(name, shape):
+def measured_traffic(name, shape, kernel=None):
     """HBM bytes per launch of a kernel, from the rocprofv3 FETCH_SIZE and
     WRITE_SIZE passes summarised in profiles/traffic.json (None if that
     kernel and shape were not profiled)."""
@@ -50,6 +51,8 @@ def measured_traffic(name, shape):
     except (OSError, ValueError):
         return None
     if not entry or list(entry.get("shape", [])) != list(shape):
+        return None
+    if kernel is not None and not entry.get("kernel", "").startswith(kernel):
         return None
     return entry.get("bytes_per_launch")
 
@@ -258,12 +261,13 @@ def headline(args, timer, rng):
         step()
     ms = timer.time(step, args.steps)
     flops = 2.0 * M * N * K
-    # the step's two kernels timed alone: the activation split pass, and the
-    # tile GEMM on the split planes (the dominant kernel)
-    from enilnets_amd.nn.dense import dense_w8_planes, split_planes
-    xp = split_planes(d_x, "fp32")
-    split_ms = timer.time(lambda i: split_planes(d_x, "fp32"), args.steps)
-    gemm_ms = timer.time(lambda i: dense_w8_planes(xp, wq, None, "linear", out=y), args.steps)
+    # the step's two kernels timed alone: the activation split pass (fp16
+    # high parts, e4m3 low parts) and the tile GEMM on its output (the
+    # dominant kernel)
+    from enilnets_amd.nn.dense import dense_w8_split, split_f16f8
+    xs = split_f16f8(d_x)
+    split_ms = timer.time(lambda i: split_f16f8(d_x), args.steps)
+    gemm_ms = timer.time(lambda i: dense_w8_split(xs, wq, None, "linear", out=y), args.steps)
     return {"x": x, "w": w, "fq": fq, "codes": codes, "scale": scale, "m": M, "n": N, "k": K,
             "ms": ms, "flops": flops, "split_ms": split_ms, "gemm_ms": gemm_ms}
 
@@ -679,7 +683,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 weights x fp32 activations (bf16 hi+lo MFMA, fp32 accumulate)",
+        "dtype": "int8 weights x fp32 activations (fp16 hi + e4m3 lo MFMA, fp32 accumulate)",
         "data": "synthetic (seeded N(0, 0.02) weight quantized per output channel, "
                 "N(0, 1) activations)",
         "config": {"workload": "configs[2]: Dense 8192x8192 int8 weight (per output channel), "
@@ -687,19 +691,21 @@ def main():
                    "m": h["m"], "n": h["n"], "k": h["k"], "variant": "fp32",
                    "flops_per_step": flops},
         "roofline": {"bound": "mfma",
-                     "kernel": "w8_ring_kernel<RingCfg<256,256,4,2,2,3,false>>",
+                     "kernel": "w8_f8_ring_kernel<F8RingCfg<256,256,4,2,3>>",
                      "shape": shape,
                      "achieved": round(flops / h["gemm_ms"] / 1e9, 3), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s",
                      "frac": round(flops / h["gemm_ms"] / 1e9 / BF16_PEAK_TFLOPS, 4),
                      "kernel_ms": round(h["gemm_ms"], 5),
                      "split_pass_ms": round(h["split_ms"], 5),
-                     "traffic": measured_traffic("w8_gemm_config2", shape),
+                     "traffic": measured_traffic("w8_gemm_config2", shape, "w8_f8_ring_kernel<F8RingCfg<256,256,4,2,3>"),
                      "note": "algorithmic 2*M*N*K over the HIP-event time of the tile GEMM "
-                             "launched alone on pre-split planes (enq_gemm_w8_planes); a step "
-                             "is the split pass (fp32 -> bf16 hi/lo planes) plus this kernel. "
-                             "The fp32-accurate path issues two bf16 MFMA passes (hi, lo) per "
-                             "product, so its own ceiling is half the bf16 peak"},
+                             "launched alone on pre-split activations (enq_gemm_w8_f16f8); a "
+                             "step is the split pass (fp32 -> fp16 hi + e4m3 lo, per-row "
+                             "power-of-two exponent) plus this kernel. Per 64-deep step the "
+                             "kernel issues 4 fp16 and 1 fp8 MFMAs per 32x32 block (1.5 bf16-"
+                             "MFMA equivalents per product), so its own ceiling is 2/3 of the "
+                             "bf16 peak"},
     }
     if not args.no_components:
         result["components"] = components(timer, rng, args.only)

@@ -669,7 +669,6 @@ struct RingCfg {
   static_assert((4 * BN) % NT == 0, "whole 8-code expansion items per thread");
 };
 
-__device__ __forceinline__ int swz32(int row, int half) { return half ^ ((row >> 3) & 1); }
 // fp32 A rows of 128 bytes (8 chunks of 16): chunk XOR bits 1-3 of the row.
 // A fragment read takes the same logical chunk of 32 consecutive rows; any
 // 16 consecutive rows then cover the 16 chunk slots of two rows' 256 bytes
@@ -1290,6 +1289,13 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
         launch_w8_ring<RingCfg<128, 128, 4, 2, P, 4, true>>(nullptr, 0, kp, codes, w_scale, bias,
                                                             m, n, k, ep, y, z, RowGroups{}, x);
       });
+    } else if (planes == 2 && f16f8_supported(k, codes)) {
+      // Large fp32-accurate GEMMs: fp16 high parts and e4m3 low parts, split
+      // in a pass of their own (a quarter fewer matrix-core cycles than the
+      // bf16 hi/lo planes)
+      void* buf = scratch_of(f16f8_bytes(m, k));
+      split_f16f8(x, m, k, buf);
+      gemm_w8_f16f8(buf, m, k, codes, w_scale, n, bias, ep, y, z);
     } else {
       // Large GEMMs split the activations in a pass of their own.  Splitting
       // them inside the 256 x 256 kernel instead (as the 128 x 128 kernel

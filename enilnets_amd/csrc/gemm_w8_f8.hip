@@ -1,0 +1,537 @@
+// fp32-accurate W8 Dense for large tiles, with the activations split into an
+// fp16 high part and an fp8 (OCP e4m3) low part.
+//
+//   e[m]  = the power of two with max_k |x[m,k]| * 2^e[m] in [2^14, 2^15)
+//   hi    = fp16(x * 2^e)                  (11 significant bits, nearest even)
+//   lo    = e4m3(x * 2^e - hi)             (|x * 2^e - hi| <= 2^-11 |x * 2^e|)
+//   acc   = sum_k hi * q  +  sum_k lo * e4m3(q)        (one fp32 accumulator)
+//   y     = act(ldexp(acc, -e[m]) * scale[n] + bias[n])
+//
+// q is the int8 weight code, exact in fp16.  The high products are exact,
+// the low part carries x's next bits to about 2^-4 of themselves, and e4m3(q)
+// is q within 1/16: the error is below 2e-5 of the row's largest output for
+// normal, uniform, heavy-tailed, log-normal and Cauchy activations (CPU
+// simulation at K = 8192), five times inside the 1e-4 * ||row||_inf bound.
+// The fp8 matrix cores take 64 K values per instruction at twice the fp16
+// rate, so a 64-deep step costs 4 fp16 + 1 fp8 MFMAs against 8 bf16 MFMAs
+// for the hi/lo bf16 split: a quarter fewer matrix-core cycles.  The row
+// exponent keeps x * 2^e inside fp16's range and the low part inside e4m3's.
+//
+// Kernels
+//   split_f16f8_kernel   x (m, k) fp32 -> hi (m, kp) fp16, lo (m, kp) e4m3,
+//                        e (m) int32; kp = k rounded up to 64, zero padded
+//   w8_f8_ring_kernel    direct-to-LDS ring GEMM: per 32-deep stage the hi,
+//                        lo and int8 code tiles, the codes expanded once per
+//                        workgroup into fp16 and e4m3 tiles; fp16 MFMAs every
+//                        stage, fp8 MFMAs every second stage on the low parts
+//                        of both stages; per-row exponent, column scale,
+//                        bias and activation in the epilogue
+#include <algorithm>
+#include <cmath>
+
+#include "common.hpp"
+#include "epilogue.hpp"
+#include "mfma.hpp"
+#include "ops.hpp"
+#include "tiling.hpp"
+
+namespace enq {
+namespace {
+
+constexpr int kF8KPad = 64;  // K of one fp8 MFMA: the planes' row padding
+
+// The row exponent e: max |x| * 2^e in [2^14, 2^15).  A zero, infinite or
+// NaN maximum gives 0 (the row's products are then zero or non-finite anyway).
+__device__ __forceinline__ int row_exponent(float amax) {
+  if (!(amax > 0.0f) || amax == __builtin_inff()) return 0;
+  int ex;
+  frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
+  return 15 - ex;
+}
+
+// Four activations -> their fp16 high parts (two dwords) and e4m3 low parts
+// (one dword), after scaling by 2^e.
+__device__ __forceinline__ void split4_f16f8(float4 v, int e, uint2& hi, uint32_t& lo) {
+  const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+  _Float16 h[4];
+  float r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = static_cast<_Float16>(a[i]);  // nearest even
+    r[i] = a[i] - static_cast<float>(h[i]);  // exact
+  }
+  hi.x = uint32_t(__builtin_bit_cast(uint16_t, h[0])) | (uint32_t(__builtin_bit_cast(uint16_t, h[1])) << 16);
+  hi.y = uint32_t(__builtin_bit_cast(uint16_t, h[2])) | (uint32_t(__builtin_bit_cast(uint16_t, h[3])) << 16);
+  int p = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
+  p = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], p, true);
+  lo = uint32_t(p);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// One 256-thread workgroup per row.  REGS: the row (k % 4 == 0, 16-byte
+// aligned, k <= 1024 * V) stays in registers between its maximum and its
+// split; otherwise it is read twice with scalar loads.
+template <int V, bool REGS>
+__global__ __launch_bounds__(256) void split_f16f8_kernel(const float* __restrict__ x, int64_t k,
+                                                          int64_t kp, uint16_t* __restrict__ hi,
+                                                          uint8_t* __restrict__ lo,
+                                                          int* __restrict__ exps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * k;
+  const int tid = threadIdx.x;
+  float amax = 0.0f;  // fmaxf skips NaN
+  float4 v[REGS ? V : 1];
+  if constexpr (REGS) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int64_t c = (int64_t(j) * 256 + tid) * 4;
+      v[j] = c < k ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
+  } else {
+    for (int64_t c = tid; c < k; c += 256) amax = fmaxf(amax, fabsf(xr[c]));
+  }
+  amax = wave_max(amax);
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const int e = row_exponent(amax);
+  if (tid == 0) exps[row] = e;
+  uint16_t* hr = hi + row * kp;
+  uint8_t* lr = lo + row * kp;
+  if constexpr (REGS) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int64_t c = (int64_t(j) * 256 + tid) * 4;
+      if (c < kp) {
+        uint2 h;
+        uint32_t l;
+        split4_f16f8(v[j], e, h, l);
+        *reinterpret_cast<uint2*>(hr + c) = h;
+        *reinterpret_cast<uint32_t*>(lr + c) = l;
+      }
+    }
+  } else {
+    for (int64_t c = int64_t(tid) * 4; c < kp; c += 1024) {
+      float4 t;
+      t.x = c < k ? xr[c] : 0.0f;
+      t.y = c + 1 < k ? xr[c + 1] : 0.0f;
+      t.z = c + 2 < k ? xr[c + 2] : 0.0f;
+      t.w = c + 3 < k ? xr[c + 3] : 0.0f;
+      uint2 h;
+      uint32_t l;
+      split4_f16f8(t, e, h, l);
+      *reinterpret_cast<uint2*>(hr + c) = h;
+      *reinterpret_cast<uint32_t*>(lr + c) = l;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The GEMM.  A stage is 32 deep: the hi tile (BM rows of 64 bytes, chunks
+// swizzled by swz64), the lo tile (BM rows of 32 bytes, halves swizzled by
+// swz32) and the int8 code tile (BN rows of 32 bytes, swz32), all filled by
+// global_load_lds_dwordx4 in 1 KiB blocks.  Each stage's codes are expanded
+// once per workgroup into an fp16 tile (64-byte rows) and an e4m3 tile
+// (32-byte rows, the same byte positions as the codes), double-buffered after
+// the ring; the expansion of stage t + 1 is issued among stage t's MFMAs.
+//
+// fp8 operands: lane group g of a 32 x 32 x 64 MFMA takes, in dwords 0-3, the
+// 16 low parts (or e4m3 codes) of logical half g of the even stage's 32-byte
+// row and, in dwords 4-7, those of the odd stage.  Which K position the
+// instruction gives each byte does not matter as long as A and B agree, and
+// they are laid out alike.
+// ---------------------------------------------------------------------------
+template <int BM_, int BN_, int WM_, int WN_, int STAGES_>
+struct F8RingCfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, STAGES = STAGES_, BK = 32;
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  static constexpr int HI_BYTES = BM * 64, LO_BYTES = BM * 32, B_BYTES = BN * 32;
+  static constexpr int A_BYTES = HI_BYTES + LO_BYTES;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int B16_BYTES = BN * 64, B8_BYTES = BN * 32;
+  static constexpr int CONV_BYTES = B16_BYTES + B8_BYTES;  // one expanded code tile
+  static constexpr int HI_BLOCKS = HI_BYTES / 1024, LO_BLOCKS = LO_BYTES / 1024;
+  static constexpr int B_BLOCKS = B_BYTES / 1024;
+  static constexpr int BLOCKS = HI_BLOCKS + LO_BLOCKS + B_BLOCKS;
+  // every wave issues the same number of blocks (vmcnt accounting); waves
+  // past the last block repeat it, rewriting identical bytes
+  static constexpr int DMA_PER_WAVE = (BLOCKS + NT / 64 - 1) / (NT / 64);
+  static_assert(HI_BYTES % 1024 == 0 && LO_BYTES % 1024 == 0 && B_BYTES % 1024 == 0,
+                "whole 1 KiB blocks");
+  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES + 2 * CONV_BYTES;
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  static constexpr int WG_PER_CU = (160 * 1024) / LDS_BYTES;
+  static constexpr int WAVES_PER_EU = (NT / 256) * WG_PER_CU < 8 ? (NT / 256) * WG_PER_CU : 8;
+  static_assert((4 * BN) % NT == 0, "whole 8-code expansion items per thread");
+  static_assert(STAGES >= 3, "two stages in flight");
+};
+
+template <class C, bool KTAIL>
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WAVES_PER_EU, C::WAVES_PER_EU)))
+void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restrict__ xl,
+                       const int* __restrict__ xe, int64_t kp, const int8_t* __restrict__ w,
+                       const float* __restrict__ scale, const float* __restrict__ bias,
+                       int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n, Epilogue ep,
+                       float* __restrict__ y, float* __restrict__ z) {
+  constexpr int BM = C::BM, BN = C::BN, WN = C::WN, STAGES = C::STAGES, BK = C::BK;
+  constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN;
+  constexpr int DPW = C::DMA_PER_WAVE;
+  extern __shared__ __align__(16) uint16_t lds_raw[];
+  char* lds = reinterpret_cast<char*>(lds_raw);
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  int tm, tn;
+  xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
+  const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
+
+  // DMA sources of this wave's blocks; kind 0: hi (16 rows x 64 B), 1: lo
+  // (32 rows x 32 B), 2: codes (32 rows x 32 B)
+  const char* src[DPW];
+  int src_koff[DPW];
+  int kind[DPW];
+#pragma unroll
+  for (int j = 0; j < DPW; ++j) {
+    const int blk = min(wave * DPW + j, C::BLOCKS - 1);
+    src_koff[j] = 0;
+    if (blk < C::HI_BLOCKS) {
+      const int r = blk * 16 + (lane >> 2);
+      int64_t g = m0 + r;
+      g = g < m ? g : m - 1;
+      src[j] = reinterpret_cast<const char*>(xh + g * kp) + 16 * swz64(r, lane & 3);
+      kind[j] = 0;
+    } else if (blk < C::HI_BLOCKS + C::LO_BLOCKS) {
+      const int r = (blk - C::HI_BLOCKS) * 32 + (lane >> 1);
+      int64_t g = m0 + r;
+      g = g < m ? g : m - 1;
+      src[j] = reinterpret_cast<const char*>(xl + g * kp) + 16 * swz32(r, lane & 1);
+      kind[j] = 1;
+    } else {
+      const int r = (blk - C::HI_BLOCKS - C::LO_BLOCKS) * 32 + (lane >> 1);
+      int64_t g = n0 + r;
+      g = g < n ? g : n - 1;
+      src[j] = reinterpret_cast<const char*>(w + g * k);
+      src_koff[j] = 16 * swz32(r, lane & 1);
+      kind[j] = 2;
+    }
+  }
+  const int ktiles = int(kp / BK);  // even: kp is a multiple of 64
+  const void* zero = g_zero16;
+  constexpr int AHEAD = STAGES - 1;
+  auto issue_blocks = [&](int t, auto j0, auto j1) {
+    const uint32_t dst = lds_addr(lds) + (t % STAGES) * C::STAGE_BYTES;
+#pragma unroll
+    for (int j = decltype(j0)::value; j < decltype(j1)::value; ++j) {
+      const int blk = min(wave * DPW + j, C::BLOCKS - 1);
+      const void* sp;
+      if (kind[j] == 0) {
+        sp = src[j] + int64_t(t) * (BK * 2);
+      } else if (kind[j] == 1) {
+        sp = src[j] + int64_t(t) * BK;
+      } else {
+        const int64_t kb = int64_t(t) * BK + src_koff[j];
+        sp = (KTAIL && kb >= k) ? zero : static_cast<const void*>(src[j] + kb);
+      }
+      dma16(sp, dst + blk * 1024);
+    }
+  };
+  constexpr int DMA_HALF = DPW / 2;
+  using JA = std::integral_constant<int, 0>;
+  using JB = std::integral_constant<int, DMA_HALF>;
+  using JC = std::integral_constant<int, DPW>;
+  auto issue = [&](int t) { issue_blocks(t, JA{}, JC{}); };
+  auto wait_stage = [&](int t, int issued) {
+    const int later = (issued < ktiles - 1 ? issued : ktiles - 1) - t;
+    wait_stages_after<DPW, AHEAD - 1>(later);
+  };
+
+  floatx16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int lrow = lane & 31, g = lane >> 5;
+  char* conv = lds + STAGES * C::STAGE_BYTES;
+  int a_off[FM][2], lo_off[FM], b_off[FN][2], b8_off[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int r = wm * TM + i * 32 + lrow;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) a_off[i][ks] = r * 64 + 16 * swz64(r, 2 * g + ks);
+    lo_off[i] = C::HI_BYTES + r * 32 + 16 * swz32(r, g);
+  }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int c = wn * TN + j * 32 + lrow;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) b_off[j][ks] = c * 64 + 16 * swz64(c, 2 * g + ks);
+    b8_off[j] = C::B16_BYTES + c * 32 + 16 * swz32(c, g);
+  }
+  // expansion items: piece q of 8 codes of code row cr (logical bytes 8 q ..
+  // 8 q + 7) -> logical chunk q of the fp16 row and the same bytes of the
+  // e4m3 row
+  constexpr int B_ITEMS = 4 * BN / C::NT;
+  int conv_src[B_ITEMS], conv_d16[B_ITEMS], conv_d8[B_ITEMS];
+#pragma unroll
+  for (int it = 0; it < B_ITEMS; ++it) {
+    const int item = tid + it * C::NT, cr = item >> 2, q = item & 3;
+    const int pos = cr * 32 + 16 * swz32(cr, q >> 1) + 8 * (q & 1);
+    conv_src[it] = C::A_BYTES + pos;
+    conv_d16[it] = cr * 64 + 16 * swz64(cr, q);
+    conv_d8[it] = C::B16_BYTES + pos;
+  }
+  uint2 craw[B_ITEMS];
+  auto convert_load = [&](int t) {
+    const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) craw[it] = *reinterpret_cast<const uint2*>(st + conv_src[it]);
+  };
+  auto convert_store = [&](int t) {
+    char* bdst = conv + (t & 1) * C::CONV_BYTES;
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) {
+      uint4 h;
+      uint2 f;
+      codes4_to_f16_e4m3(craw[it].x, h.x, h.y, f.x);
+      codes4_to_f16_e4m3(craw[it].y, h.z, h.w, f.y);
+      *reinterpret_cast<uint4*>(bdst + conv_d16[it]) = h;
+      *reinterpret_cast<uint2*>(bdst + conv_d8[it]) = f;
+    }
+  };
+  // one set of fp16 fragments, read per k-step just before its MFMAs (the
+  // previous step's MFMAs cover the reads); the fp8 halves are read last
+  halfx8 fa[FM], fb[FN];
+  intx8 la[FM], lb[FN];  // fp8 operands: even stage in dwords 0-3, odd in 4-7
+  auto read_hi = [&](int t, int ks) {
+    const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
+    const char* bt = conv + (t & 1) * C::CONV_BYTES;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const halfx8*>(st + a_off[i][ks]);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) fb[j] = *reinterpret_cast<const halfx8*>(bt + b_off[j][ks]);
+  };
+  auto read_lo = [&](int t, auto odd) {
+    const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
+    const char* bt = conv + (t & 1) * C::CONV_BYTES;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const intx4 v = *reinterpret_cast<const intx4*>(st + lo_off[i]);
+      if constexpr (decltype(odd)::value) la[i].hi = v;
+      else la[i].lo = v;
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const intx4 v = *reinterpret_cast<const intx4*>(bt + b8_off[j]);
+      if constexpr (decltype(odd)::value) lb[j].hi = v;
+      else lb[j].lo = v;
+    }
+  };
+
+#pragma unroll
+  for (int s0 = 0; s0 < AHEAD; ++s0)
+    if (s0 < ktiles) issue(s0);
+  wait_stage(0, AHEAD - 1);
+  block_barrier();
+  convert_load(0);
+  convert_store(0);
+
+  // Iteration t: once every wave's copy of stage t + 1 has landed and the
+  // expansion of stage t is written, a barrier; then issue stage t + AHEAD
+  // (in two groups), read stage t's fragments and stage t + 1's raw codes,
+  // run stage t's fp16 MFMAs (and, at odd t, the fp8 MFMAs of stages t - 1
+  // and t), and expand stage t + 1 into the other buffer while they execute.
+  auto stage = [&](int t, auto steady, auto odd) {
+    if constexpr (decltype(steady)::value)
+      wait_vmcnt<(AHEAD - 2) * DPW>();  // stages t+2 .. t+AHEAD-1 may fly
+    else if (t + 1 < ktiles)
+      wait_stage(t + 1, t + AHEAD - 1);
+    wait_lgkmcnt0();  // this wave's expansion writes of stage t are done
+    block_barrier();
+    const bool refill = decltype(steady)::value || t + AHEAD < ktiles;
+    if (refill) issue_blocks(t + AHEAD, JA{}, JB{});
+    auto f16_step = [&]() {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma_32x32x16_f16(fa[i], fb[j], acc[i][j]);
+    };
+    read_hi(t, 0);
+    convert_load(t + 1);
+    issue_fence();
+    f16_step();
+    sched_fence();
+    read_hi(t, 1);
+    issue_fence();
+    if (refill) issue_blocks(t + AHEAD, JB{}, JC{});
+    sched_fence();
+    f16_step();
+    sched_fence();
+    read_lo(t, odd);
+    issue_fence();
+    if constexpr (decltype(odd)::value) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma_32x32x64_e4m3(la[i], lb[j], acc[i][j]);
+    }
+    convert_store(t + 1);
+    sched_fence();
+  };
+  using Even = std::false_type;
+  using Odd = std::true_type;
+  int t = 0;
+  if constexpr (AHEAD > 2)
+    for (; t + 1 + AHEAD < ktiles; t += 2) {
+      stage(t, std::true_type{}, Even{});
+      stage(t + 1, std::true_type{}, Odd{});
+    }
+  for (; t < ktiles; t += 2) {
+    stage(t, std::false_type{}, Even{});
+    stage(t + 1, std::false_type{}, Odd{});
+  }
+
+  const int lhalf = lane >> 5;
+  with_activation<false>(ep, [&](auto act) {
+    static_for<0, FM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      int ex[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * lhalf + (e % 4);
+        ex[e] = -xe[row < m ? row : m - 1];
+      }
+      const int64_t row0 = m0 + wm * TM + i * 32 + 4 * lhalf;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int64_t col = n0 + wn * TN + j * 32 + lrow;
+        if (col >= n) continue;
+        const float s = scale[col];
+        const float b = bias ? bias[col] : 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int64_t row = row0 + 8 * (e / 4) + (e % 4);
+          if (row < m) {
+            float v = ldexpf(acc[i][j][e], ex[e]) * s;
+            if (bias) v = v + b;
+            if (z) z[row * n + col] = v;
+            y[row * n + col] = act(v);
+          }
+        }
+      }
+    });
+  });
+}
+
+template <class C>
+void launch_w8_f8(const uint16_t* xh, const uint8_t* xl, const int* xe, int64_t kp,
+                  const int8_t* w, const float* scale, const float* bias, int64_t m, int64_t n,
+                  int64_t k, const Epilogue& ep, float* y, float* z) {
+  const int64_t tiles_m = ceil_div(m, C::BM), tiles_n = ceil_div(n, C::BN);
+  ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
+  const size_t lds_bytes = size_t(C::LDS_BYTES);
+  static bool attr_set = false;
+  if (!attr_set) {
+    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8_f8_ring_kernel<C, false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
+    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8_f8_ring_kernel<C, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
+    attr_set = true;
+  }
+  auto kernel = (k % C::BK == 0) ? w8_f8_ring_kernel<C, false> : w8_f8_ring_kernel<C, true>;
+  kernel<<<unsigned(tiles_m * tiles_n), C::NT, lds_bytes, stream()>>>(
+      xh, xl, xe, kp, w, scale, bias, m, n, k, int(tiles_m), int(tiles_n), ep, y, z);
+  check_launch("w8_f8_ring_kernel");
+}
+
+// 256 x 256 tiles (3 stages) when they fill the device, else 128 x 128 (4 stages)
+using F8Big = F8RingCfg<256, 256, 4, 2, 3>;
+using F8Mid = F8RingCfg<128, 128, 4, 2, 4>;
+
+struct F16F8View {
+  uint16_t* hi;
+  uint8_t* lo;
+  int* exps;
+};
+
+F16F8View f16f8_view(void* buf, int64_t m, int64_t kp) {
+  char* p = static_cast<char*>(buf);
+  return {reinterpret_cast<uint16_t*>(p), reinterpret_cast<uint8_t*>(p + 2 * m * kp),
+          reinterpret_cast<int*>(p + 3 * m * kp)};
+}
+
+}  // namespace
+
+int64_t f16f8_k_pad(int64_t k) { return ceil_div(k, kF8KPad) * kF8KPad; }
+
+size_t f16f8_bytes(int64_t m, int64_t k) { return size_t(m) * size_t(3 * f16f8_k_pad(k) + 4); }
+
+bool f16f8_supported(int64_t k, const int8_t* codes) {
+  return k % 16 == 0 && aligned(codes, 16);
+}
+
+void split_f16f8(const float* x, int64_t m, int64_t k, void* buf) {
+  ENQ_REQUIRE(m <= 0x7fffffff, "too many rows");
+  ENQ_REQUIRE(aligned(buf, 16), "split buffer must be 16-byte aligned");
+  const int64_t kp = f16f8_k_pad(k);
+  const F16F8View v = f16f8_view(buf, m, kp);
+  if (k % 4 == 0 && aligned(x, 16) && k <= 8192)
+    split_f16f8_kernel<8, true><<<unsigned(m), 256, 0, stream()>>>(x, k, kp, v.hi, v.lo, v.exps);
+  else
+    split_f16f8_kernel<1, false><<<unsigned(m), 256, 0, stream()>>>(x, k, kp, v.hi, v.lo, v.exps);
+  check_launch("split_f16f8_kernel");
+}
+
+void gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes,
+                   const float* w_scale, int64_t n, const float* bias, const Epilogue& ep,
+                   float* y, float* z) {
+  ENQ_REQUIRE(f16f8_supported(k, codes),
+              "the fp16/fp8 split GEMM needs K a multiple of 16 and 16-byte aligned codes");
+  ENQ_REQUIRE(aligned(buf, 16), "split buffer must be 16-byte aligned");
+  const int64_t kp = f16f8_k_pad(k);
+  const F16F8View v = f16f8_view(const_cast<void*>(buf), m, kp);
+  const bool big = ceil_div(m, 256) * ceil_div(n, 256) >= device_cu_count();
+  if (big)
+    launch_w8_f8<F8Big>(v.hi, v.lo, v.exps, kp, codes, w_scale, bias, m, n, k, ep, y, z);
+  else
+    launch_w8_f8<F8Mid>(v.hi, v.lo, v.exps, kp, codes, w_scale, bias, m, n, k, ep, y, z);
+}
+
+}  // namespace enq
+
+using namespace enq;
+
+extern "C" int enq_split_f16f8(const float* x, int64_t m, int64_t k, void* buf) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && k >= 1, "m and k must be positive (m=%lld k=%lld)", (long long)m,
+                (long long)k);
+    ENQ_REQUIRE(x && buf, "NULL pointer argument");
+    split_f16f8(x, m, k, buf);
+  });
+}
+
+extern "C" int enq_gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes,
+                                 const float* w_scale, int64_t n, const float* bias,
+                                 int activation, float act_alpha, float act_clip, float* y,
+                                 float* z) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && n >= 1 && k >= 1, "m, n, k must be positive (m=%lld n=%lld k=%lld)",
+                (long long)m, (long long)n, (long long)k);
+    ENQ_REQUIRE(buf && codes && w_scale && y, "NULL pointer argument");
+    ENQ_REQUIRE(valid_activation(activation), "unknown activation code %d", activation);
+    const Epilogue ep{activation, act_alpha, act_clip};
+    gemm_w8_f16f8(buf, m, k, codes, w_scale, n, bias, gemm_epilogue(ep, false), y, z);
+    finish_rows(y, m, n, ep, false);
+  });
+}

@@ -18,9 +18,13 @@
 namespace enq {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
+typedef short shortx2 __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef int intx4 __attribute__((ext_vector_type(4)));
+typedef int intx8 __attribute__((ext_vector_type(8)));
 typedef int intx16 __attribute__((ext_vector_type(16)));
 
 struct alignas(16) Pack8 {
@@ -32,6 +36,17 @@ __device__ __forceinline__ floatx16 mfma_32x32x16_bf16(bf16x8 a, bf16x8 b, float
 }
 __device__ __forceinline__ floatx4 mfma_16x16x32_bf16(bf16x8 a, bf16x8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx16 mfma_32x32x16_f16(halfx8 a, halfx8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+// fp8 (OCP e4m3) x fp8, 32 x 32 x 64: each operand is 32 values in eight
+// dwords.  Both block-scale operands zero selects the unscaled instruction.
+// The products of one instruction are summed in a fixed-point window about
+// 2^-15.5 of the largest of them before the sum meets the fp32 accumulator,
+// which is added exactly (measured on gfx950).
+__device__ __forceinline__ floatx16 mfma_32x32x64_e4m3(intx8 a, intx8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 // int8: each operand is 16 codes packed in four dwords.
 __device__ __forceinline__ intx16 mfma_32x32x32_i8(intx4 a, intx4 b, intx16 c) {
@@ -73,6 +88,26 @@ __device__ __forceinline__ bf16x8 codes8_to_bf16(uint32_t lo, uint32_t hi) {
   codes4_to_bf16(lo, d[0], d[1]);
   codes4_to_bf16(hi, d[2], d[3]);
   return __builtin_bit_cast(bf16x8, d);
+}
+
+// Four signed int8 codes (one dword) -> four fp16 values, exactly, and their
+// four e4m3 bytes.  The fp16 with bits 0x64uu is 1024 + uu, so placing
+// u = q + 128 (the code with its sign bit flipped) under 0x64 and
+// subtracting 1152 gives q; e4m3 keeps four significant bits of |q| > 16,
+// rounded to nearest even (127 -> 128).
+__device__ __forceinline__ void codes4_to_f16_e4m3(uint32_t word, uint32_t& h01, uint32_t& h23,
+                                                   uint32_t& f8) {
+  const uint32_t u = word ^ 0x80808080u;
+  const halfx2 bias = {_Float16(1152.0f), _Float16(1152.0f)};
+  // v_perm_b32: selector bytes 0-3 pick from the second operand, 4-7 from the first
+  const halfx2 a = __builtin_bit_cast(halfx2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
+  const halfx2 b = __builtin_bit_cast(halfx2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+  h01 = __builtin_bit_cast(uint32_t, a);
+  h23 = __builtin_bit_cast(uint32_t, b);
+  shortx2 p = {0, 0};
+  p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(p, a, 1.0f, false);
+  p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(p, b, 1.0f, true);
+  f8 = __builtin_bit_cast(uint32_t, p);
 }
 
 // 16 int8 codes -> two groups of 8 bf16 (codes 0..7 and 8..15).

@@ -25,6 +25,20 @@ void split_planes(const float* x, const int* gather, int64_t m, int64_t k, uint1
 // K padding of the planes the LDS-tiled GEMM reads.
 int64_t gemm_k_pad(int64_t k);
 
+// fp32-accurate split of the large-tile W8 GEMM (gemm_w8_f8.hip): x (m, k)
+// -> fp16 high parts (m, kp), e4m3 low parts (m, kp) and a power-of-two row
+// exponent (m int32), packed in that order into f16f8_bytes(m, k) bytes;
+// kp = f16f8_k_pad(k).
+int64_t f16f8_k_pad(int64_t k);
+size_t f16f8_bytes(int64_t m, int64_t k);
+bool f16f8_supported(int64_t k, const int8_t* codes);
+void split_f16f8(const float* x, int64_t m, int64_t k, void* buf);
+// act(x @ (codes * w_scale).T + bias) from split_f16f8's buffer; the
+// epilogue's fake-quantization is not applied (gemm_epilogue(ep, false)).
+void gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes,
+                   const float* w_scale, int64_t n, const float* bias, const Epilogue& ep,
+                   float* y, float* z);
+
 // Whether the grouped GEMM takes weights of this K and alignment.
 bool grouped_gemm_supported(int64_t k, const int8_t* codes);
 

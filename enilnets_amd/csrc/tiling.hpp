@@ -136,6 +136,10 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
 // ds_read_b128 when lanes 0..31 read 32 consecutive rows at one chunk.
 __device__ __forceinline__ int swz64(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
 
+// The same for the two 16-byte halves of a 32-byte LDS row: 16 consecutive
+// rows read at one logical half touch every bank once.
+__device__ __forceinline__ int swz32(int row, int half) { return half ^ ((row >> 3) & 1); }
+
 // Zero bytes (static storage is zero-initialised): the DMA source for chunks
 // past the end of K.  One copy per translation unit.
 static __device__ __align__(16) int4 g_zero16[4];

@@ -164,6 +164,52 @@ def dense_w8_planes(xp: ActivationPlanes, w: Int8Weights, bias: Optional[DeviceA
     return y
 
 
+class SplitActivations:
+    """Activations split once for the large-tile fp32-accurate GEMM
+    (``split_f16f8``): fp16 high parts, e4m3 low parts and a power-of-two
+    exponent per row, for several ``dense_w8_split`` calls."""
+
+    def __init__(self, data: DeviceArray, shape: Tuple[int, ...]):
+        self.data, self.shape = data, shape
+
+
+def split_f16f8(x: DeviceArray) -> SplitActivations:
+    """The fp32-accurate split of fp32 ``x`` (``..., k``): per row the power of
+    two e with max |x| * 2^e in [2^14, 2^15), hi = fp16(x * 2^e) and
+    lo = e4m3(x * 2^e - hi), rows padded to a multiple of 64."""
+    if x.dtype != np.float32:
+        raise NotImplementedError(f"W8 Dense takes float32 activations, got {x.dtype}")
+    m, k = _rows(x)
+    kp = -(-k // 64) * 64
+    buf = DeviceArray((m * (3 * kp + 4),), np.uint8)
+    _lib.call("enq_split_f16f8", x.ptr, m, k, buf.ptr)
+    return SplitActivations(buf, x.shape)
+
+
+def dense_w8_split(xs: SplitActivations, w: Int8Weights, bias: Optional[DeviceArray] = None,
+                   activation: str = "linear",
+                   activation_params: Optional[Dict[str, Any]] = None,
+                   out: Optional[DeviceArray] = None,
+                   pre_activation: Optional[DeviceArray] = None) -> DeviceArray:
+    """``dense_w8`` (fp32-accurate) on activations already split by
+    ``split_f16f8``: the large-tile GEMM of ``dense_w8`` without the split.
+    Needs K a multiple of 16."""
+    k = xs.shape[-1]
+    m = int(np.prod(xs.shape[:-1], dtype=np.int64))
+    n, wk = w.shape[-2], w.shape[-1]
+    if len(w.shape) != 2:
+        raise ValueError(f"dense weights must be 2-D, got shape {w.shape}")
+    if wk != k:
+        raise ValueError(f"shapes {xs.shape} and {w.shape} not aligned: {k} (dim -1) != {wk}")
+    code, alpha, clip = activation_args(activation, activation_params)
+    y = out if out is not None else DeviceArray(xs.shape[:-1] + (n,), np.float32)
+    z = pre_activation.ptr if pre_activation is not None else null()
+    b = bias.ptr if bias is not None else null()
+    _lib.call("enq_gemm_w8_f16f8", xs.data.ptr, m, k, w.codes.ptr, w.scale.ptr, n, b, code,
+              alpha, clip, y.ptr, z)
+    return y
+
+
 def dense_w8a8(x: DeviceArray, w: Int8Weights, bias: Optional[DeviceArray] = None,
                activation: str = "linear", activation_params: Optional[Dict[str, Any]] = None,
                out: Optional[DeviceArray] = None,

@@ -235,6 +235,23 @@ int enq_gemm_w8_planes(const uint16_t* planes, int64_t m, int64_t k, const int8_
                        const float* w_scale, int64_t n, const float* bias, int activation,
                        float act_alpha, float act_clip, int variant, float* y, float* z);
 
+/* The two halves of enq_dense_w8's fp32-accurate path for large tiles (k a
+ * multiple of 16, 16-byte aligned codes), for callers that multiply one batch
+ * of activations by several weights.  enq_split_f16f8 writes, per row of x
+ * (m, k) fp32, the power of two e with max |x| * 2^e in [2^14, 2^15), the
+ * fp16 high parts hi = fp16(x * 2^e) and the e4m3 low parts
+ * lo = e4m3(x * 2^e - hi), rows padded with zeros to kp = k rounded up to a
+ * multiple of 64: hi (m, kp) uint16 at buf, lo (m, kp) bytes at
+ * buf + 2 * m * kp, e (m) int32 at buf + 3 * m * kp; buf holds
+ * m * (3 * kp + 4) bytes, 16-byte aligned.  enq_gemm_w8_f16f8 computes
+ * enq_dense_w8's y and z from that buffer, within 1e-4 * max |z| per row of
+ * the float64 product (no activation fake-quantization).  No counterpart in
+ * the reference: they split the Dense of forward.py:318-321 in two. */
+int enq_split_f16f8(const float* x, int64_t m, int64_t k, void* buf);
+int enq_gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes,
+                      const float* w_scale, int64_t n, const float* bias, int activation,
+                      float act_alpha, float act_clip, float* y, float* z);
+
 /* enq_dense_w8 without any allocation.  No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same

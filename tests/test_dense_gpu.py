@@ -132,9 +132,90 @@ def test_dense_w8_on_split_planes(gpu, m, k, n, variant, tol):
         z_ref = x[pick].astype(np.float64) @ fq.astype(np.float64).T + b
         assert np.all(row_rel_err(zh[pick].astype(np.float64), z_ref) <= tol)
         assert np.allclose(y, oracle.activate(act, zh.astype(np.float64)), rtol=2e-6, atol=2e-6)
-        if (m + 255) // 256 * ((n + 255) // 256) >= 256:
+        if variant == "bf16" and (m + 255) // 256 * ((n + 255) // 256) >= 256:
+            # (the large fp32 tiles of dense_w8 take the fp16 / e4m3 split,
+            # compared with dense_w8_split below)
             y2 = D.dense_w8(d_x, wq, d_b, act, variant=variant).numpy()
             assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+
+
+def e4m3_round(v):
+    """Nearest OCP e4m3 value (bias 7, 3 mantissa bits, subnormals down to
+    2^-9), ties to even; |v| stays below the format's 448 here."""
+    v = np.asarray(v, np.float64)
+    a = np.abs(v)
+    ex = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    ulp = np.exp2(np.maximum(ex, -6.0) - 3.0)
+    return np.sign(v) * np.round(a / ulp) * ulp
+
+
+def e4m3_value(b):
+    b = np.asarray(b, np.uint8).astype(np.int64)
+    s, e, f = b >> 7, (b >> 3) & 15, b & 7
+    mag = np.where(e == 0, np.ldexp(f / 8.0, -6), np.ldexp(1.0 + f / 8.0, e - 7))
+    return np.where(s == 1, -mag, mag)
+
+
+def wide_rows(m, k, seed):
+    """Activation rows of very different kinds: normal, a zero row, rows
+    scaled by 1e-30 and 1e30, heavy-tailed (Cauchy), log-normal magnitudes,
+    a row with a few outliers a thousand times the rest."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k))
+    kinds = np.arange(m) % 7
+    x[kinds == 1] = 0.0
+    x[kinds == 2] *= 1e-30
+    x[kinds == 3] *= 1e30
+    x[kinds == 4] = rng.standard_cauchy((int(np.sum(kinds == 4)), k))
+    x[kinds == 5] *= np.exp(rng.normal(0.0, 3.0, (int(np.sum(kinds == 5)), k)))
+    x[kinds == 6, : min(k, 8)] *= 1000.0
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("m,k", [(9, 8192), (7, 100), (7, 1040), (7, 9000)])
+def test_split_f16f8_layout(gpu, m, k):
+    # the split of the large-tile fp32 path, element by element: the row
+    # exponent, hi = fp16(x * 2^e) and lo = e4m3(x * 2^e - hi), zero padding
+    print(f"[case] split_f16f8 m={m} k={k}", flush=True)
+    x = wide_rows(m, k, seed=m + k)
+    buf = D.split_f16f8(DeviceArray.from_numpy(x)).data.numpy()
+    kp = -(-k // 64) * 64
+    hi = buf[: 2 * m * kp].view(np.uint16).reshape(m, kp)
+    lo = buf[2 * m * kp: 3 * m * kp].reshape(m, kp)
+    ex = buf[3 * m * kp:].view(np.int32)
+    amax = np.max(np.abs(x), axis=1)
+    want_e = np.where(amax > 0, 15 - np.frexp(np.where(amax > 0, amax, 1.0))[1], 0)
+    assert np.array_equal(ex, want_e)
+    xs = np.ldexp(x, want_e[:, None]).astype(np.float32)
+    h = xs.astype(np.float16)
+    assert np.array_equal(hi[:, :k], h.view(np.uint16))
+    r = (xs - h.astype(np.float32)).astype(np.float64)
+    assert np.array_equal(e4m3_value(lo[:, :k]), e4m3_round(r))
+    assert not hi[:, k:].any() and not lo[:, k:].any()
+
+
+@pytest.mark.parametrize("m,k,n", [(4096, 1024, 4096), (4100, 1040, 4100), (4097, 2048, 4095),
+                                   (300, 784, 1024), (129, 48, 260), (65, 64, 32)])
+def test_dense_w8_split(gpu, m, k, n):
+    # the fp16 / e4m3 split GEMM within the fp32 bound on rows of every kind,
+    # and, where dense_w8 takes it (tiles that fill the device), bit-identical
+    # to dense_w8
+    print(f"[case] dense_w8_split m={m} k={k} n={n}", flush=True)
+    _, fq, codes, rows, b, wq = make(m, k, n, seed=3 * m + k + n, wstd=0.03)
+    x = wide_rows(m, k, seed=m + n)
+    d_x, d_b = DeviceArray.from_numpy(x), DeviceArray.from_numpy(b)
+    xs = D.split_f16f8(d_x)
+    z = DeviceArray((m, n), np.float32)
+    y = D.dense_w8_split(xs, wq, d_b, "relu", pre_activation=z).numpy()
+    zh = z.numpy()
+    pick = np.unique(np.concatenate([np.arange(0, m, 29), np.arange(m - 8, m)]))
+    z_ref = x[pick].astype(np.float64) @ fq.astype(np.float64).T + b
+    err = row_rel_err(zh[pick].astype(np.float64), z_ref)
+    assert np.all(err <= 1e-4), f"max row error {err.max():.3e}"
+    assert np.array_equal(y, np.maximum(zh, 0))
+    if (m + 255) // 256 * ((n + 255) // 256) >= 256:
+        y2 = D.dense_w8(d_x, wq, d_b, "relu").numpy()
+        assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
 
 
 @pytest.mark.parametrize("act", ["relu", "leakyrelu", "elu", "selu", "gelu", "swish", "mish",
