@@ -134,13 +134,21 @@ __global__ __launch_bounds__(256) void split_f16f8_kernel(const float* __restric
 }
 
 // ---------------------------------------------------------------------------
-// The GEMM.  A stage is 32 deep: the hi tile (BM rows of 64 bytes, chunks
-// swizzled by swz64), the lo tile (BM rows of 32 bytes, halves swizzled by
-// swz32) and the int8 code tile (BN rows of 32 bytes, swz32), all filled by
-// global_load_lds_dwordx4 in 1 KiB blocks.  Each stage's codes are expanded
-// once per workgroup into an fp16 tile (64-byte rows) and an e4m3 tile
-// (32-byte rows, the same byte positions as the codes), double-buffered after
-// the ring; the expansion of stage t + 1 is issued among stage t's MFMAs.
+// The GEMM.  A stage is 32 deep.  Its A tile (the hi parts, BM rows of 64
+// bytes with chunks swizzled by swz64, then the lo parts, BM rows of 32 bytes
+// with halves swizzled by swz32) and its code tile (BN rows of 32 bytes,
+// swz32) go global -> LDS by global_load_lds_dwordx4 in 1 KiB blocks, into
+// two rings: A tiles are multiplied AHEAD stages after their DMA is issued,
+// while code tiles are expanded a stage before they are multiplied, so the
+// code ring runs one stage further ahead and holds one slot more.  Each
+// wave's DMA of iteration t, group G(t + AHEAD), is its share of A tile
+// t + AHEAD and of code tile t + AHEAD + 1; the top of iteration t waits for
+// G(t), issued AHEAD iterations earlier, with a fixed vmcnt.  Groups past the
+// end of K load the zero block into slots no one reads again, so every
+// iteration has the same wait.  Each stage's codes are expanded once per
+// workgroup into an fp16 tile (64-byte rows) and an e4m3 tile (32-byte rows,
+// the codes' own byte positions), double-buffered after the rings; the
+// expansion of stage t + 1 is issued among stage t's MFMAs.
 //
 // fp8 operands: lane group g of a 32 x 32 x 64 MFMA takes, in dwords 0-3, the
 // 16 low parts (or e4m3 codes) of logical half g of the even stage's 32-byte
@@ -148,30 +156,33 @@ __global__ __launch_bounds__(256) void split_f16f8_kernel(const float* __restric
 // instruction gives each byte does not matter as long as A and B agree, and
 // they are laid out alike.
 // ---------------------------------------------------------------------------
-template <int BM_, int BN_, int WM_, int WN_, int STAGES_>
+template <int BM_, int BN_, int WM_, int WN_, int AHEAD_>
 struct F8RingCfg {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, STAGES = STAGES_, BK = 32;
-  static constexpr int NT = WM * WN * 64;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, AHEAD = AHEAD_, BK = 32;
+  static constexpr int NT = WM * WN * 64, WAVES = NT / 64;
   static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
   static constexpr int HI_BYTES = BM * 64, LO_BYTES = BM * 32, B_BYTES = BN * 32;
   static constexpr int A_BYTES = HI_BYTES + LO_BYTES;
-  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int A_SLOTS = AHEAD + 1, B_SLOTS = AHEAD + 2;
   static constexpr int B16_BYTES = BN * 64, B8_BYTES = BN * 32;
   static constexpr int CONV_BYTES = B16_BYTES + B8_BYTES;  // one expanded code tile
-  static constexpr int HI_BLOCKS = HI_BYTES / 1024, LO_BLOCKS = LO_BYTES / 1024;
+  static constexpr int HI_BLOCKS = HI_BYTES / 1024, A_BLOCKS = A_BYTES / 1024;
   static constexpr int B_BLOCKS = B_BYTES / 1024;
-  static constexpr int BLOCKS = HI_BLOCKS + LO_BLOCKS + B_BLOCKS;
-  // every wave issues the same number of blocks (vmcnt accounting); waves
-  // past the last block repeat it, rewriting identical bytes
-  static constexpr int DMA_PER_WAVE = (BLOCKS + NT / 64 - 1) / (NT / 64);
   static_assert(HI_BYTES % 1024 == 0 && LO_BYTES % 1024 == 0 && B_BYTES % 1024 == 0,
                 "whole 1 KiB blocks");
-  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES + 2 * CONV_BYTES;
+  // every wave issues the same number of blocks (vmcnt accounting); waves
+  // past the last block repeat it, rewriting identical bytes
+  static constexpr int A_PW = (A_BLOCKS + WAVES - 1) / WAVES;
+  static constexpr int B_PW = (B_BLOCKS + WAVES - 1) / WAVES;
+  static constexpr int DPW = A_PW + B_PW;
+  static constexpr int B_RING = A_SLOTS * A_BYTES;            // byte offset of the code ring
+  static constexpr int CONV = B_RING + B_SLOTS * B_BYTES;     // of the expanded tiles
+  static constexpr int LDS_BYTES = CONV + 2 * CONV_BYTES;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
   static constexpr int WG_PER_CU = (160 * 1024) / LDS_BYTES;
   static constexpr int WAVES_PER_EU = (NT / 256) * WG_PER_CU < 8 ? (NT / 256) * WG_PER_CU : 8;
   static_assert((4 * BN) % NT == 0, "whole 8-code expansion items per thread");
-  static_assert(STAGES >= 3, "two stages in flight");
+  static_assert(AHEAD >= 2 && AHEAD * DPW < 64, "vmcnt range");
 };
 
 template <class C, bool KTAIL>
@@ -181,9 +192,9 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
                        const float* __restrict__ scale, const float* __restrict__ bias,
                        int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n, Epilogue ep,
                        float* __restrict__ y, float* __restrict__ z) {
-  constexpr int BM = C::BM, BN = C::BN, WN = C::WN, STAGES = C::STAGES, BK = C::BK;
+  constexpr int BM = C::BM, BN = C::BN, WN = C::WN, AHEAD = C::AHEAD, BK = C::BK;
   constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN;
-  constexpr int DPW = C::DMA_PER_WAVE;
+  constexpr int A_PW = C::A_PW, B_PW = C::B_PW, DPW = C::DPW;
   extern __shared__ __align__(16) uint16_t lds_raw[];
   char* lds = reinterpret_cast<char*>(lds_raw);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -192,65 +203,77 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
   xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
   const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
 
-  // DMA sources of this wave's blocks; kind 0: hi (16 rows x 64 B), 1: lo
-  // (32 rows x 32 B), 2: codes (32 rows x 32 B)
-  const char* src[DPW];
-  int src_koff[DPW];
-  int kind[DPW];
+  // DMA sources of this wave's blocks, as 32-bit byte offsets from the
+  // planes' (or codes') base: A blocks (hi: 16 rows x 64 B, lo: 32 rows x
+  // 32 B) and code blocks (32 rows x 32 B)
+  uint32_t a_voff[A_PW];
+  bool a_hi[A_PW];
 #pragma unroll
-  for (int j = 0; j < DPW; ++j) {
-    const int blk = min(wave * DPW + j, C::BLOCKS - 1);
-    src_koff[j] = 0;
+  for (int j = 0; j < A_PW; ++j) {
+    const int blk = min(wave * A_PW + j, C::A_BLOCKS - 1);
     if (blk < C::HI_BLOCKS) {
       const int r = blk * 16 + (lane >> 2);
       int64_t g = m0 + r;
       g = g < m ? g : m - 1;
-      src[j] = reinterpret_cast<const char*>(xh + g * kp) + 16 * swz64(r, lane & 3);
-      kind[j] = 0;
-    } else if (blk < C::HI_BLOCKS + C::LO_BLOCKS) {
+      a_voff[j] = uint32_t(g * kp * 2 + 16 * swz64(r, lane & 3));
+      a_hi[j] = true;
+    } else {
       const int r = (blk - C::HI_BLOCKS) * 32 + (lane >> 1);
       int64_t g = m0 + r;
       g = g < m ? g : m - 1;
-      src[j] = reinterpret_cast<const char*>(xl + g * kp) + 16 * swz32(r, lane & 1);
-      kind[j] = 1;
-    } else {
-      const int r = (blk - C::HI_BLOCKS - C::LO_BLOCKS) * 32 + (lane >> 1);
-      int64_t g = n0 + r;
-      g = g < n ? g : n - 1;
-      src[j] = reinterpret_cast<const char*>(w + g * k);
-      src_koff[j] = 16 * swz32(r, lane & 1);
-      kind[j] = 2;
+      a_voff[j] = uint32_t(g * kp + 16 * swz32(r, lane & 1));
+      a_hi[j] = false;
     }
+  }
+  uint32_t b_voff[B_PW];
+  int b_koff[B_PW];
+#pragma unroll
+  for (int j = 0; j < B_PW; ++j) {
+    const int blk = min(wave * B_PW + j, C::B_BLOCKS - 1);
+    const int r = blk * 32 + (lane >> 1);
+    int64_t g = n0 + r;
+    g = g < n ? g : n - 1;
+    b_koff[j] = 16 * swz32(r, lane & 1);
+    b_voff[j] = uint32_t(g * k + b_koff[j]);
   }
   const int ktiles = int(kp / BK);  // even: kp is a multiple of 64
   const void* zero = g_zero16;
-  constexpr int AHEAD = STAGES - 1;
-  auto issue_blocks = [&](int t, auto j0, auto j1) {
-    const uint32_t dst = lds_addr(lds) + (t % STAGES) * C::STAGE_BYTES;
+  const uint32_t lds0 = lds_addr(lds);
+  const char* xh_b = reinterpret_cast<const char*>(xh);
+  const char* xl_b = reinterpret_cast<const char*>(xl);
+  const char* w_b = reinterpret_cast<const char*>(w);
+  // block j (< A_PW: A, else codes) of this wave's group G(s): A tile s and
+  // code tile s + 1.  Tiles past the end of K reload the last one into a
+  // slot no one reads again (uniform wait counts).
+  auto dma_a = [&](int s, int j) {
+    const int blk = min(wave * A_PW + j, C::A_BLOCKS - 1);
+    const int64_t sc = s < ktiles ? s : ktiles - 1;
+    const char* base = a_hi[j] ? xh_b + sc * (2 * BK) : xl_b + sc * BK;
+    dma16_s(a_voff[j], base, lds0 + (s % C::A_SLOTS) * C::A_BYTES + blk * 1024);
+  };
+  auto dma_b = [&](int s, int j) {
+    const int blk = min(wave * B_PW + j, C::B_BLOCKS - 1);
+    const int64_t sc = s < ktiles ? s : ktiles - 1;
+    const uint32_t dst = lds0 + C::B_RING + (s % C::B_SLOTS) * C::B_BYTES + blk * 1024;
+    if constexpr (KTAIL) {
+      // 16-byte chunks past k read the zero block
+      const bool live = sc * BK + b_koff[j] < k;
+      dma16(live ? static_cast<const void*>(w_b + b_voff[j] + sc * BK) : zero, dst);
+    } else {
+      dma16_s(b_voff[j], w_b + sc * BK, dst);
+    }
+  };
+  auto issue_group = [&](int s, auto j0, auto j1) {
 #pragma unroll
     for (int j = decltype(j0)::value; j < decltype(j1)::value; ++j) {
-      const int blk = min(wave * DPW + j, C::BLOCKS - 1);
-      const void* sp;
-      if (kind[j] == 0) {
-        sp = src[j] + int64_t(t) * (BK * 2);
-      } else if (kind[j] == 1) {
-        sp = src[j] + int64_t(t) * BK;
-      } else {
-        const int64_t kb = int64_t(t) * BK + src_koff[j];
-        sp = (KTAIL && kb >= k) ? zero : static_cast<const void*>(src[j] + kb);
-      }
-      dma16(sp, dst + blk * 1024);
+      if (j < A_PW) dma_a(s, j);
+      else dma_b(s + 1, j - A_PW);
     }
   };
   constexpr int DMA_HALF = DPW / 2;
   using JA = std::integral_constant<int, 0>;
   using JB = std::integral_constant<int, DMA_HALF>;
   using JC = std::integral_constant<int, DPW>;
-  auto issue = [&](int t) { issue_blocks(t, JA{}, JC{}); };
-  auto wait_stage = [&](int t, int issued) {
-    const int later = (issued < ktiles - 1 ? issued : ktiles - 1) - t;
-    wait_stages_after<DPW, AHEAD - 1>(later);
-  };
 
   floatx16 acc[FM][FN];
 #pragma unroll
@@ -261,7 +284,7 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   const int lrow = lane & 31, g = lane >> 5;
-  char* conv = lds + STAGES * C::STAGE_BYTES;
+  char* conv = lds + C::CONV;
   int a_off[FM][2], lo_off[FM], b_off[FN][2], b8_off[FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
@@ -281,18 +304,16 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
   // 8 q + 7) -> logical chunk q of the fp16 row and the same bytes of the
   // e4m3 row
   constexpr int B_ITEMS = 4 * BN / C::NT;
-  int conv_src[B_ITEMS], conv_d16[B_ITEMS], conv_d8[B_ITEMS];
+  int conv_src[B_ITEMS], conv_d16[B_ITEMS];
 #pragma unroll
   for (int it = 0; it < B_ITEMS; ++it) {
     const int item = tid + it * C::NT, cr = item >> 2, q = item & 3;
-    const int pos = cr * 32 + 16 * swz32(cr, q >> 1) + 8 * (q & 1);
-    conv_src[it] = C::A_BYTES + pos;
+    conv_src[it] = cr * 32 + 16 * swz32(cr, q >> 1) + 8 * (q & 1);
     conv_d16[it] = cr * 64 + 16 * swz64(cr, q);
-    conv_d8[it] = C::B16_BYTES + pos;
   }
   uint2 craw[B_ITEMS];
   auto convert_load = [&](int t) {
-    const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
+    const char* st = lds + C::B_RING + (t % C::B_SLOTS) * C::B_BYTES;
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) craw[it] = *reinterpret_cast<const uint2*>(st + conv_src[it]);
   };
@@ -305,23 +326,26 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
       codes4_to_f16_e4m3(craw[it].x, h.x, h.y, f.x);
       codes4_to_f16_e4m3(craw[it].y, h.z, h.w, f.y);
       *reinterpret_cast<uint4*>(bdst + conv_d16[it]) = h;
-      *reinterpret_cast<uint2*>(bdst + conv_d8[it]) = f;
+      *reinterpret_cast<uint2*>(bdst + C::B16_BYTES + conv_src[it]) = f;
     }
   };
-  // one set of fp16 fragments, read per k-step just before its MFMAs (the
-  // previous step's MFMAs cover the reads); the fp8 halves are read last
-  halfx8 fa[FM], fb[FN];
+  // two sets of fp16 fragments, one per k-step: k-step 1 of stage t is read
+  // at the top of iteration t and multiplied after the barrier that ends it,
+  // while k-step 0 of stage t + 1 is read, so the matrix cores have work
+  // queued across the barrier; the fp8 halves are read after k-step 0's MFMAs
+  halfx8 fa[2][FM], fb[2][FN];
   intx8 la[FM], lb[FN];  // fp8 operands: even stage in dwords 0-3, odd in 4-7
-  auto read_hi = [&](int t, int ks) {
-    const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
+  auto read_hi = [&](int t, auto ksc) {
+    constexpr int ks = decltype(ksc)::value;
+    const char* st = lds + (t % C::A_SLOTS) * C::A_BYTES;
     const char* bt = conv + (t & 1) * C::CONV_BYTES;
 #pragma unroll
-    for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const halfx8*>(st + a_off[i][ks]);
+    for (int i = 0; i < FM; ++i) fa[ks][i] = *reinterpret_cast<const halfx8*>(st + a_off[i][ks]);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) fb[j] = *reinterpret_cast<const halfx8*>(bt + b_off[j][ks]);
+    for (int j = 0; j < FN; ++j) fb[ks][j] = *reinterpret_cast<const halfx8*>(bt + b_off[j][ks]);
   };
   auto read_lo = [&](int t, auto odd) {
-    const char* st = lds + (t % STAGES) * C::STAGE_BYTES;
+    const char* st = lds + (t % C::A_SLOTS) * C::A_BYTES;
     const char* bt = conv + (t & 1) * C::CONV_BYTES;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -337,47 +361,49 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
     }
   };
 
+  // prologue: code tile 0, then groups G(0) .. G(AHEAD - 1); tile 0's codes
+  // are expanded once they land
 #pragma unroll
-  for (int s0 = 0; s0 < AHEAD; ++s0)
-    if (s0 < ktiles) issue(s0);
-  wait_stage(0, AHEAD - 1);
+  for (int j = 0; j < B_PW; ++j) dma_b(0, j);
+#pragma unroll
+  for (int s = 0; s < AHEAD; ++s) issue_group(s, JA{}, JC{});
+  wait_vmcnt<AHEAD * DPW>();
   block_barrier();
   convert_load(0);
   convert_store(0);
 
-  // Iteration t: once every wave's copy of stage t + 1 has landed and the
-  // expansion of stage t is written, a barrier; then issue stage t + AHEAD
-  // (in two groups), read stage t's fragments and stage t + 1's raw codes,
-  // run stage t's fp16 MFMAs (and, at odd t, the fp8 MFMAs of stages t - 1
-  // and t), and expand stage t + 1 into the other buffer while they execute.
-  auto stage = [&](int t, auto steady, auto odd) {
-    if constexpr (decltype(steady)::value)
-      wait_vmcnt<(AHEAD - 2) * DPW>();  // stages t+2 .. t+AHEAD-1 may fly
-    else if (t + 1 < ktiles)
-      wait_stage(t + 1, t + AHEAD - 1);
-    wait_lgkmcnt0();  // this wave's expansion writes of stage t are done
-    block_barrier();
-    const bool refill = decltype(steady)::value || t + AHEAD < ktiles;
-    if (refill) issue_blocks(t + AHEAD, JA{}, JB{});
-    auto f16_step = [&]() {
+  using KS0 = std::integral_constant<int, 0>;
+  using KS1 = std::integral_constant<int, 1>;
+  auto f16_step = [&](auto ksc) {
+    constexpr int ks = decltype(ksc)::value;
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma_32x32x16_f16(fa[i], fb[j], acc[i][j]);
-    };
-    read_hi(t, 0);
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma_32x32x16_f16(fa[ks][i], fb[ks][j], acc[i][j]);
+  };
+  // stage 0: G(0) landed for every wave, its codes expanded; k-step 0 read
+  wait_vmcnt<(AHEAD - 1) * DPW>();
+  wait_lgkmcnt0();
+  block_barrier();
+  read_hi(0, KS0{});
+
+  // Iteration t (k-step 0 of stage t already read): issue G(t + AHEAD) in
+  // two groups, read k-step 1 and stage t + 1's raw codes, run k-step 0's
+  // MFMAs, read the fp8 halves (and at odd t run the fp8 MFMAs of stages
+  // t - 1 and t), expand stage t + 1 into the other buffer; then, once G(t +
+  // 1) has landed for this wave and its expansion writes are done, the
+  // barrier; read k-step 0 of stage t + 1 and run k-step 1's MFMAs.
+  auto stage = [&](int t, auto odd) {
+    issue_group(t + AHEAD, JA{}, JB{});
+    read_hi(t, KS1{});
     convert_load(t + 1);
     issue_fence();
-    f16_step();
-    sched_fence();
-    read_hi(t, 1);
-    issue_fence();
-    if (refill) issue_blocks(t + AHEAD, JB{}, JC{});
-    sched_fence();
-    f16_step();
+    f16_step(KS0{});
     sched_fence();
     read_lo(t, odd);
     issue_fence();
+    issue_group(t + AHEAD, JB{}, JC{});
+    sched_fence();
     if constexpr (decltype(odd)::value) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -386,19 +412,22 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
     }
     convert_store(t + 1);
     sched_fence();
+    wait_vmcnt<(AHEAD - 1) * DPW>();  // G(t + 2) .. G(t + AHEAD) may fly
+    wait_lgkmcnt0();
+    block_barrier();
+    // (past the last stage this reads slots no one writes again: unused)
+    read_hi(t + 1, KS0{});
+    issue_fence();
+    f16_step(KS1{});
+    sched_fence();
   };
-  using Even = std::false_type;
-  using Odd = std::true_type;
-  int t = 0;
-  if constexpr (AHEAD > 2)
-    for (; t + 1 + AHEAD < ktiles; t += 2) {
-      stage(t, std::true_type{}, Even{});
-      stage(t + 1, std::true_type{}, Odd{});
-    }
-  for (; t < ktiles; t += 2) {
-    stage(t, std::false_type{}, Even{});
-    stage(t + 1, std::false_type{}, Odd{});
+  for (int t = 0; t < ktiles; t += 2) {
+    stage(t, std::false_type{});
+    stage(t + 1, std::true_type{});
   }
+  // every DMA of this wave has landed before the workgroup ends (the last
+  // groups wrote slots no one reads)
+  wait_vmcnt<0>();
 
   const int lhalf = lane >> 5;
   with_activation<false>(ep, [&](auto act) {
@@ -453,9 +482,10 @@ void launch_w8_f8(const uint16_t* xh, const uint8_t* xl, const int* xe, int64_t 
   check_launch("w8_f8_ring_kernel");
 }
 
-// 256 x 256 tiles (3 stages) when they fill the device, else 128 x 128 (4 stages)
-using F8Big = F8RingCfg<256, 256, 4, 2, 3>;
-using F8Mid = F8RingCfg<128, 128, 4, 2, 4>;
+// 256 x 256 tiles (two stages ahead) when they fill the device, else 128 x 128
+// (three ahead)
+using F8Big = F8RingCfg<256, 256, 4, 2, 2>;
+using F8Mid = F8RingCfg<128, 128, 4, 2, 3>;
 
 struct F16F8View {
   uint16_t* hi;
@@ -498,6 +528,9 @@ void gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes,
               "the fp16/fp8 split GEMM needs K a multiple of 16 and 16-byte aligned codes");
   ENQ_REQUIRE(aligned(buf, 16), "split buffer must be 16-byte aligned");
   const int64_t kp = f16f8_k_pad(k);
+  // the kernel addresses the planes and the codes by 32-bit byte offsets
+  ENQ_REQUIRE(2 * m * kp < (int64_t(1) << 32) && n * k < (int64_t(1) << 32),
+              "fp16/fp8 split GEMM operands above 4 GiB");
   const F16F8View v = f16f8_view(const_cast<void*>(buf), m, kp);
   const bool big = ceil_div(m, 256) * ceil_div(n, 256) >= device_cu_count();
   if (big)

@@ -130,6 +130,15 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
                : "v"(src), "s"(lds_base)
                : "memory", "m0");
 }
+// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
+// byte offset (the instruction's saddr form): one VGPR per source instead of
+// two, and no per-lane address arithmetic when the base advances.
+__device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // XOR swizzle of the four 16-byte chunks of a 64-byte LDS row: conflict-free
