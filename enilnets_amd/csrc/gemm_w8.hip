@@ -1263,7 +1263,14 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
   // the GEMV finish kernel and the 128 x 128 kernel fuse the activation
   // fake-quantization; the other GEMM kernels leave it to finish_rows
   const bool big = ceil_div(m, 256) * ceil_div(n, 256) >= device_cu_count();
-  const bool fused_mid = !gemv && !big && kmode != 2 && k % 4 == 0 && aligned(x, 16);
+  // fp32-accurate GEMMs of more than 2^33 multiply-adds take the fp16 / e4m3
+  // split even below the 256 x 256 tile count: its pass over x costs less
+  // than the in-register split saves there (4096 x 3072 x 1024: 86.9 against
+  // 94.8 us; 4096 x 1024 x 4096: 98.0 against 108.9), while the MLP layers
+  // (4096 x 1024 x 1024: 38.5 against 33.2 us) keep the fused kernel
+  const bool split_f8 = !gemv && planes == 2 && f16f8_supported(k, codes) &&
+                        (big || double(m) * double(n) * double(k) > 8589934592.0);
+  const bool fused_mid = !gemv && !big && !split_f8 && kmode != 2 && k % 4 == 0 && aligned(x, 16);
   const bool fuse_aq = gemv || fused_mid;
   const Epilogue ep = gemm_epilogue(ep_all, fuse_aq);
   if (gemv) {
@@ -1289,10 +1296,10 @@ void dense_w8(const float* x, int64_t m, int64_t k, const int8_t* codes, const f
         launch_w8_ring<RingCfg<128, 128, 4, 2, P, 4, true>>(nullptr, 0, kp, codes, w_scale, bias,
                                                             m, n, k, ep, y, z, RowGroups{}, x);
       });
-    } else if (planes == 2 && f16f8_supported(k, codes)) {
-      // Large fp32-accurate GEMMs: fp16 high parts and e4m3 low parts, split
-      // in a pass of their own (a quarter fewer matrix-core cycles than the
-      // bf16 hi/lo planes)
+    } else if (split_f8) {
+      // fp32-accurate: fp16 high parts and e4m3 low parts, split in a pass of
+      // their own (a quarter fewer matrix-core cycles than the bf16 hi/lo
+      // planes)
       void* buf = scratch_of(f16f8_bytes(m, k));
       split_f16f8(x, m, k, buf);
       gemm_w8_f16f8(buf, m, k, codes, w_scale, n, bias, ep, y, z);

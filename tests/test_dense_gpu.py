@@ -195,11 +195,12 @@ def test_split_f16f8_layout(gpu, m, k):
 
 
 @pytest.mark.parametrize("m,k,n", [(4096, 1024, 4096), (4100, 1040, 4100), (4097, 2048, 4095),
-                                   (300, 784, 1024), (129, 48, 260), (65, 64, 32)])
+                                   (1024, 2304, 4096), (300, 784, 1024), (129, 48, 260),
+                                   (65, 64, 32)])
 def test_dense_w8_split(gpu, m, k, n):
     # the fp16 / e4m3 split GEMM within the fp32 bound on rows of every kind,
-    # and, where dense_w8 takes it (tiles that fill the device), bit-identical
-    # to dense_w8
+    # and, where dense_w8 takes it (tiles that fill the device, or more than
+    # 2^33 multiply-adds), bit-identical to dense_w8
     print(f"[case] dense_w8_split m={m} k={k} n={n}", flush=True)
     _, fq, codes, rows, b, wq = make(m, k, n, seed=3 * m + k + n, wstd=0.03)
     x = wide_rows(m, k, seed=m + n)
@@ -213,7 +214,7 @@ def test_dense_w8_split(gpu, m, k, n):
     err = row_rel_err(zh[pick].astype(np.float64), z_ref)
     assert np.all(err <= 1e-4), f"max row error {err.max():.3e}"
     assert np.array_equal(y, np.maximum(zh, 0))
-    if (m + 255) // 256 * ((n + 255) // 256) >= 256:
+    if (m + 255) // 256 * ((n + 255) // 256) >= 256 or m * n * k > 2 ** 33:
         y2 = D.dense_w8(d_x, wq, d_b, "relu").numpy()
         assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
 
