@@ -691,14 +691,14 @@ def main():
                    "m": h["m"], "n": h["n"], "k": h["k"], "variant": "fp32",
                    "flops_per_step": flops},
         "roofline": {"bound": "mfma",
-                     "kernel": "w8_f8_ring_kernel<F8RingCfg<256,256,4,2,3>>",
+                     "kernel": "w8_f8_ring_kernel<F8RingCfg<256,256,4,2,2>>",
                      "shape": shape,
                      "achieved": round(flops / h["gemm_ms"] / 1e9, 3), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s",
                      "frac": round(flops / h["gemm_ms"] / 1e9 / BF16_PEAK_TFLOPS, 4),
                      "kernel_ms": round(h["gemm_ms"], 5),
                      "split_pass_ms": round(h["split_ms"], 5),
-                     "traffic": measured_traffic("w8_gemm_config2", shape, "w8_f8_ring_kernel<F8RingCfg<256,256,4,2,3>"),
+                     "traffic": measured_traffic("w8_gemm_config2", shape, "w8_f8_ring_kernel<F8RingCfg<256,256,4,2,2>"),
                      "note": "algorithmic 2*M*N*K over the HIP-event time of the tile GEMM "
                              "launched alone on pre-split activations (enq_gemm_w8_f16f8); a "
                              "step is the split pass (fp32 -> fp16 hi + e4m3 lo, per-row "
