@@ -256,13 +256,14 @@ int enq_gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
  * arguments, kernels and results as enq_dense_w8; the GEMV partial sums and
- * bf16 activation planes some shapes need come from a fixed 64 MiB device
- * array per device instead of the growable workspace.  A call that needs
- * more (GEMV partials: 4 * K-slices * n * rows rounded up to 16, 32 or 64
- * for m <= 64, to a multiple of 16 above; activation planes, taken by the
- * bf16 variant at 256 x 256 tiles and by unaligned activations: 2 * planes *
- * m * k rounded up to a multiple of 32) fails with
- * ENQ_ERR_INVALID before launching anything.  Calls that overlap on one
+ * split activations some shapes need come from a fixed 64 MiB device array
+ * per device instead of the growable workspace.  A call that needs more
+ * (GEMV partials: 4 * K-slices * n * rows rounded up to 16, 32 or 64 for
+ * m <= 64, to a multiple of 16 above; the fp32-accurate variant's fp16 / e4m3
+ * split of large GEMMs: m * (3 * kp + 4) with kp = k rounded up to 64;
+ * bf16 activation planes, taken by the bf16 variant at 256 x 256 tiles and
+ * by unaligned activations: 2 * planes * m * k rounded up to a multiple of
+ * 32) fails with ENQ_ERR_INVALID before launching anything.  Calls that overlap on one
  * device share that array and race: issue them on one stream, in order. */
 int enq_dense_w8_noalloc(const float* x, int64_t m, int64_t k, const int8_t* codes,
                          const float* w_scale, int64_t n, const float* bias,
