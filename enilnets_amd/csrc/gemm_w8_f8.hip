@@ -73,36 +73,69 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
 // One 256-thread workgroup per row.  REGS: the row (k % 4 == 0, 16-byte
 // aligned, k <= 1024 * V) stays in registers between its maximum and its
-// split; otherwise it is read twice with scalar loads.
+// split; otherwise it is read twice with scalar loads.  Row r of the split
+// comes from row gather[r] of x (gather == nullptr: row r).  With `bound`,
+// the row also gets a second exponent, exps2[r], for a GEMM output computed
+// from it: that of the bound sum_k |x| * bound[0] + bound[1] on every output
+// of the row (f16f8_bound_params).
 template <int V, bool REGS>
-__global__ __launch_bounds__(256) void split_f16f8_kernel(const float* __restrict__ x, int64_t k,
-                                                          int64_t kp, uint16_t* __restrict__ hi,
+__global__ __launch_bounds__(256) void split_f16f8_kernel(const float* __restrict__ x,
+                                                          const int* __restrict__ gather,
+                                                          int64_t k, int64_t kp,
+                                                          uint16_t* __restrict__ hi,
                                                           uint8_t* __restrict__ lo,
-                                                          int* __restrict__ exps) {
-  __shared__ float red[4];
+                                                          int* __restrict__ exps,
+                                                          const float* __restrict__ bound,
+                                                          int* __restrict__ exps2) {
+  __shared__ float red[4], red_sum[4];
   const int64_t row = blockIdx.x;
-  const float* xr = x + row * k;
+  const float* xr = x + (gather ? int64_t(gather[row]) : row) * k;
   const int tid = threadIdx.x;
   float amax = 0.0f;  // fmaxf skips NaN
+  float l1 = 0.0f;
   float4 v[REGS ? V : 1];
   if constexpr (REGS) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int64_t c = (int64_t(j) * 256 + tid) * 4;
       v[j] = c < k ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+      const float ax = fabsf(v[j].x), ay = fabsf(v[j].y), az = fabsf(v[j].z), aw = fabsf(v[j].w);
+      amax = fmaxf(amax, fmaxf(fmaxf(ax, ay), fmaxf(az, aw)));
+      if (bound) l1 += (ax + ay) + (az + aw);
     }
   } else {
-    for (int64_t c = tid; c < k; c += 256) amax = fmaxf(amax, fabsf(xr[c]));
+    for (int64_t c = tid; c < k; c += 256) {
+      const float ax = fabsf(xr[c]);
+      amax = fmaxf(amax, ax);
+      if (bound) l1 += ax;
+    }
   }
   amax = wave_max(amax);
-  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  if (bound) l1 = wave_sum(l1);
+  if ((tid & 63) == 0) {
+    red[tid >> 6] = amax;
+    red_sum[tid >> 6] = l1;
+  }
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const int e = row_exponent(amax);
-  if (tid == 0) exps[row] = e;
+  if (tid == 0) {
+    exps[row] = e;
+    if (bound) {
+      // a float sum of |x| is within k * 2^-24 of the exact one; the bound
+      // is only an upper limit for the output's scale, so the margin is ample
+      const float total = ((red_sum[0] + red_sum[1]) + (red_sum[2] + red_sum[3])) * 1.01f;
+      exps2[row] = row_exponent(total * bound[0] + bound[1]);
+    }
+  }
   uint16_t* hr = hi + row * kp;
   uint8_t* lr = lo + row * kp;
   if constexpr (REGS) {
@@ -130,6 +163,37 @@ __global__ __launch_bounds__(256) void split_f16f8_kernel(const float* __restric
       *reinterpret_cast<uint2*>(hr + c) = h;
       *reinterpret_cast<uint32_t*>(lr + c) = l;
     }
+  }
+}
+
+// The constants of split_f16f8_kernel's output bound for a Dense
+// act(scale[n] * sum_k x_k q_nk + bias[n]) with |q| <= 127:
+//   |out| <= c * (127 * max scale * sum_k |x_k| + max |bias|) + 2 c,
+//   c = 1.07 * max(1, |alpha|),
+// which covers every activation of the epilogue (|act(z)| <= |z| for linear,
+// relu, gelu, swish, mish; leaky slopes; elu / selu, sigmoid, tanh and
+// softplus add at most 1.76).  One workgroup.
+__global__ __launch_bounds__(256) void f16f8_bound_kernel(const float* __restrict__ scale,
+                                                          int64_t ns,
+                                                          const float* __restrict__ bias,
+                                                          int64_t nb, float c,
+                                                          float* __restrict__ out) {
+  __shared__ float red_s[4], red_b[4];
+  float ms = 0.0f, mb = 0.0f;
+  for (int64_t i = threadIdx.x; i < ns; i += 256) ms = fmaxf(ms, fabsf(scale[i]));
+  for (int64_t i = threadIdx.x; i < nb; i += 256) mb = fmaxf(mb, fabsf(bias[i]));
+  ms = wave_max(ms);
+  mb = wave_max(mb);
+  if ((threadIdx.x & 63) == 0) {
+    red_s[threadIdx.x >> 6] = ms;
+    red_b[threadIdx.x >> 6] = mb;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    ms = fmaxf(fmaxf(red_s[0], red_s[1]), fmaxf(red_s[2], red_s[3]));
+    mb = fmaxf(fmaxf(red_b[0], red_b[1]), fmaxf(red_b[2], red_b[3]));
+    out[0] = c * 127.0f * ms;
+    out[1] = c * (mb + 2.0f);
   }
 }
 
@@ -185,13 +249,23 @@ struct F8RingCfg {
   static_assert(AHEAD >= 2 && AHEAD * DPW < 64, "vmcnt range");
 };
 
-template <class C, bool KTAIL>
+// The output as the next GEMM's split (YF8 instantiations): row r of the
+// (m, n) output, activated, scaled by 2^exps[r] and split into fp16 high and
+// e4m3 low parts at hi / lo + r * ld.
+struct F8Out {
+  uint16_t* hi = nullptr;
+  uint8_t* lo = nullptr;
+  const int* exps = nullptr;
+  int64_t ld = 0;
+};
+
+template <class C, bool KTAIL, bool YF8 = false>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WAVES_PER_EU, C::WAVES_PER_EU)))
 void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restrict__ xl,
                        const int* __restrict__ xe, int64_t kp, const int8_t* __restrict__ w,
                        const float* __restrict__ scale, const float* __restrict__ bias,
-                       int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n, Epilogue ep,
-                       float* __restrict__ y, float* __restrict__ z) {
+                       int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n, RowGroups grp,
+                       Epilogue ep, float* __restrict__ y, float* __restrict__ z, F8Out yo) {
   constexpr int BM = C::BM, BN = C::BN, WN = C::WN, AHEAD = C::AHEAD, BK = C::BK;
   constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN;
   constexpr int A_PW = C::A_PW, B_PW = C::B_PW, DPW = C::DPW;
@@ -201,7 +275,17 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
   const int wm = wave / WN, wn = wave % WN;
   int tm, tn;
   xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
-  const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
+  int64_t m0 = int64_t(tm) * BM, m_end = m;
+  const int64_t n0 = int64_t(tn) * BN;
+  if (grp.offsets) {
+    // grouped rows: tile row tm lives in the group whose tile range holds
+    // it; workgroups past the last group's tiles have nothing to do
+    const int e = group_tile(grp, BM, tm, m0, m_end);
+    if (e < 0) return;
+    w += int64_t(e) * grp.w_stride;
+    scale += int64_t(e) * grp.v_stride;
+    if (bias) bias += int64_t(e) * grp.v_stride;
+  }
 
   // DMA sources of this wave's blocks, as 32-bit byte offsets from the
   // planes' (or codes') base: A blocks (hi: 16 rows x 64 B, lo: 32 rows x
@@ -430,11 +514,12 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
   with_activation<false>(ep, [&](auto act) {
     static_for<0, FM>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
-      int ex[16];
+      int ex[16], eo[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * lhalf + (e % 4);
         ex[e] = -xe[row < m ? row : m - 1];
+        if constexpr (YF8) eo[e] = yo.exps[row < m ? row : m - 1];
       }
       const int64_t row0 = m0 + wm * TM + i * 32 + 4 * lhalf;
 #pragma unroll
@@ -446,11 +531,20 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int64_t row = row0 + 8 * (e / 4) + (e % 4);
-          if (row < m) {
+          if (row < m_end) {
             float v = ldexpf(acc[i][j][e], ex[e]) * s;
             if (bias) v = v + b;
-            if (z) z[row * n + col] = v;
-            y[row * n + col] = act(v);
+            if constexpr (YF8) {
+              // the next GEMM's split of this output (split4_f16f8's arithmetic)
+              const float a = ldexpf(act(v), eo[e]);
+              const _Float16 h = static_cast<_Float16>(a);
+              yo.hi[row * yo.ld + col] = __builtin_bit_cast(uint16_t, h);
+              yo.lo[row * yo.ld + col] =
+                  uint8_t(__builtin_amdgcn_cvt_pk_fp8_f32(a - static_cast<float>(h), 0.0f, 0, false));
+            } else {
+              if (z) z[row * n + col] = v;
+              y[row * n + col] = act(v);
+            }
           }
         }
       }
@@ -461,21 +555,27 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
 template <class C>
 void launch_w8_f8(const uint16_t* xh, const uint8_t* xl, const int* xe, int64_t kp,
                   const int8_t* w, const float* scale, const float* bias, int64_t m, int64_t n,
-                  int64_t k, const Epilogue& ep, float* y, float* z) {
-  const int64_t tiles_m = ceil_div(m, C::BM), tiles_n = ceil_div(n, C::BN);
+                  int64_t k, const Epilogue& ep, float* y, float* z,
+                  const RowGroups& grp = RowGroups{}, const F8Out& yo = F8Out{}) {
+  // grouped rows: every group may end in a partial tile
+  const int64_t tiles_m = ceil_div(m, C::BM) + (grp.offsets ? grp.groups : 0);
+  const int64_t tiles_n = ceil_div(n, C::BN);
   ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
   const size_t lds_bytes = size_t(C::LDS_BYTES);
   static bool attr_set = false;
   if (!attr_set) {
-    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8_f8_ring_kernel<C, false>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
-    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(w8_f8_ring_kernel<C, true>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
+    for (const void* f : {reinterpret_cast<const void*>(w8_f8_ring_kernel<C, false>),
+                          reinterpret_cast<const void*>(w8_f8_ring_kernel<C, true>),
+                          reinterpret_cast<const void*>(w8_f8_ring_kernel<C, false, true>),
+                          reinterpret_cast<const void*>(w8_f8_ring_kernel<C, true, true>)})
+      ENQ_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
     attr_set = true;
   }
   auto kernel = (k % C::BK == 0) ? w8_f8_ring_kernel<C, false> : w8_f8_ring_kernel<C, true>;
+  if (yo.hi)
+    kernel = (k % C::BK == 0) ? w8_f8_ring_kernel<C, false, true> : w8_f8_ring_kernel<C, true, true>;
   kernel<<<unsigned(tiles_m * tiles_n), C::NT, lds_bytes, stream()>>>(
-      xh, xl, xe, kp, w, scale, bias, m, n, k, int(tiles_m), int(tiles_n), ep, y, z);
+      xh, xl, xe, kp, w, scale, bias, m, n, k, int(tiles_m), int(tiles_n), grp, ep, y, z, yo);
   check_launch("w8_f8_ring_kernel");
 }
 
@@ -506,16 +606,26 @@ bool f16f8_supported(int64_t k, const int8_t* codes) {
   return k % 16 == 0 && aligned(codes, 16);
 }
 
-void split_f16f8(const float* x, int64_t m, int64_t k, void* buf) {
+void split_f16f8(const float* x, int64_t m, int64_t k, void* buf, const int* gather,
+                 const float* bound, int* exps2) {
   ENQ_REQUIRE(m <= 0x7fffffff, "too many rows");
   ENQ_REQUIRE(aligned(buf, 16), "split buffer must be 16-byte aligned");
   const int64_t kp = f16f8_k_pad(k);
   const F16F8View v = f16f8_view(buf, m, kp);
   if (k % 4 == 0 && aligned(x, 16) && k <= 8192)
-    split_f16f8_kernel<8, true><<<unsigned(m), 256, 0, stream()>>>(x, k, kp, v.hi, v.lo, v.exps);
+    split_f16f8_kernel<8, true><<<unsigned(m), 256, 0, stream()>>>(x, gather, k, kp, v.hi, v.lo,
+                                                                   v.exps, bound, exps2);
   else
-    split_f16f8_kernel<1, false><<<unsigned(m), 256, 0, stream()>>>(x, k, kp, v.hi, v.lo, v.exps);
+    split_f16f8_kernel<1, false><<<unsigned(m), 256, 0, stream()>>>(x, gather, k, kp, v.hi, v.lo,
+                                                                    v.exps, bound, exps2);
   check_launch("split_f16f8_kernel");
+}
+
+void f16f8_bound_params(const float* w_scale, int64_t ns, const float* bias, int64_t nb,
+                        const Epilogue& ep, float* out) {
+  const float c = 1.07f * fmaxf(1.0f, fabsf(ep.alpha));
+  f16f8_bound_kernel<<<1, 256, 0, stream()>>>(w_scale, ns, bias, bias ? nb : 0, c, out);
+  check_launch("f16f8_bound_kernel");
 }
 
 void gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes,
@@ -536,6 +646,27 @@ void gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes,
     launch_w8_f8<F8Mid>(v.hi, v.lo, v.exps, kp, codes, w_scale, bias, m, n, k, ep, y, z);
 }
 
+void gemm_w8_f16f8_grouped(const void* buf, int64_t m, int64_t k, const int8_t* codes,
+                           const float* w_scale, int64_t n, const float* bias,
+                           const RowGroups& grp, const Epilogue& ep, float* y, void* out_split) {
+  ENQ_REQUIRE(f16f8_supported(k, codes),
+              "the fp16/fp8 split GEMM needs K a multiple of 16 and 16-byte aligned codes");
+  ENQ_REQUIRE(ep.aq == ENQ_AQ_NONE && ep.activation != ENQ_ACT_SOFTMAX,
+              "grouped split GEMM epilogue: no softmax, no fake-quantization");
+  const int64_t kp = f16f8_k_pad(k);
+  ENQ_REQUIRE(2 * m * kp < (int64_t(1) << 32) && n * k < (int64_t(1) << 32),
+              "fp16/fp8 split GEMM operands above 4 GiB");
+  const F16F8View v = f16f8_view(const_cast<void*>(buf), m, kp);
+  F8Out yo{};
+  if (out_split) {
+    ENQ_REQUIRE(n % kF8KPad == 0, "split outputs need N a multiple of 64");
+    const F16F8View o = f16f8_view(out_split, m, n);
+    yo = F8Out{o.hi, o.lo, o.exps, n};
+  }
+  launch_w8_f8<F8Big>(v.hi, v.lo, v.exps, kp, codes, w_scale, bias, m, n, k, ep, y, nullptr, grp,
+                      yo);
+}
+
 }  // namespace enq
 
 using namespace enq;
@@ -546,7 +677,7 @@ extern "C" int enq_split_f16f8(const float* x, int64_t m, int64_t k, void* buf) 
     ENQ_REQUIRE(m >= 1 && k >= 1, "m and k must be positive (m=%lld k=%lld)", (long long)m,
                 (long long)k);
     ENQ_REQUIRE(x && buf, "NULL pointer argument");
-    split_f16f8(x, m, k, buf);
+    split_f16f8(x, m, k, buf, nullptr, nullptr, nullptr);
   });
 }
 

@@ -366,6 +366,13 @@ void moe_w8(const MoeArgs& a) {
   const int E = int(a.experts);
   const bool grouped = grouped_gemm_supported(a.d, a.w1) && grouped_gemm_supported(a.hidden, a.w2);
   const int64_t kp1 = gemm_k_pad(a.d), kp2 = gemm_k_pad(a.hidden);
+  // fp32-accurate expert GEMMs on the fp16 / e4m3 split: the gathered token
+  // rows are split once, the first GEMM writes the hidden activations as the
+  // second's split (their row exponents come from a bound computed in the
+  // first split), and neither GEMM reads bf16 planes
+  const bool split8 = grouped && planes == 2 && f16f8_supported(a.d, a.w1) &&
+                      f16f8_supported(a.hidden, a.w2) && a.hidden % 64 == 0 &&
+                      a.ep.aq == ENQ_AQ_NONE && a.ep.activation != ENQ_ACT_SOFTMAX;
 
   // sizes first (null base), then the real carve of one workspace block
   auto layout = [&](char* base, auto&& use) {
@@ -379,20 +386,25 @@ void moe_w8(const MoeArgs& a) {
     int* row_token = c.take<int>(entries);
     int* entry_pos = c.take<int>(entries);
     double* terms = c.take<double>(E);
-    uint16_t* planes1 = grouped ? c.take<uint16_t>(int64_t(planes) * entries * kp1) : nullptr;
+    const bool pl = grouped && !split8;
+    uint16_t* planes1 = pl ? c.take<uint16_t>(int64_t(planes) * entries * kp1) : nullptr;
     float* xg = grouped ? nullptr : c.take<float>(entries * a.d);
-    float* h = c.take<float>(entries * a.hidden);
-    uint16_t* planes2 = grouped ? c.take<uint16_t>(int64_t(planes) * entries * kp2) : nullptr;
+    float* h = split8 ? nullptr : c.take<float>(entries * a.hidden);
+    uint16_t* planes2 = pl ? c.take<uint16_t>(int64_t(planes) * entries * kp2) : nullptr;
     float* yg = c.take<float>(entries * a.d);
+    char* split1 = split8 ? c.take<char>(int64_t(f16f8_bytes(entries, a.d))) : nullptr;
+    char* split2 = split8 ? c.take<char>(int64_t(f16f8_bytes(entries, a.hidden))) : nullptr;
+    float* bound = split8 ? c.take<float>(2) : nullptr;
     use(c.used(), logits, probs, chosen, gates, hist, offsets, row_token, entry_pos, terms,
-        planes1, xg, h, planes2, yg);
+        planes1, xg, h, planes2, yg, split1, split2, bound);
   };
   size_t bytes = 0;
   layout(nullptr, [&](size_t used, auto...) { bytes = used; });
   char* ws = static_cast<char*>(workspace(bytes, kLayerSlot));
   layout(ws, [&](size_t, float* logits, float* probs, int* chosen, float* gates, int* hist,
                  int* offsets, int* row_token, int* entry_pos, double* terms, uint16_t* planes1,
-                 float* xg, float* h, uint16_t* planes2, float* yg) {
+                 float* xg, float* h, uint16_t* planes2, float* yg, char* split1, char* split2,
+                 float* bound) {
     if (a.logits) logits = const_cast<float*>(a.logits);
     if (a.probs) probs = a.probs;
     hipStream_t s = stream();
@@ -419,7 +431,18 @@ void moe_w8(const MoeArgs& a) {
     check_launch("moe_place_kernel");
 
     const Epilogue lin{ENQ_ACT_LINEAR, 0.0f, 0.0f};
-    if (grouped) {
+    if (split8) {
+      RowGroups g1{offsets, E, a.hidden * a.d, a.hidden};
+      RowGroups g2{offsets, E, a.d * a.hidden, a.d};
+      // the second split's exponents sit after its two planes
+      int* exps2 = reinterpret_cast<int*>(split2 + 3 * entries * f16f8_k_pad(a.hidden));
+      f16f8_bound_params(a.s1, E * a.hidden, a.b1, E * a.hidden, a.ep, bound);
+      split_f16f8(a.x, entries, a.d, split1, row_token, bound, exps2);
+      gemm_w8_f16f8_grouped(split1, entries, a.d, a.w1, a.s1, a.hidden, a.b1, g1, a.ep, nullptr,
+                            split2);
+      gemm_w8_f16f8_grouped(split2, entries, a.hidden, a.w2, a.s2, a.d, a.b2, g2, lin, yg,
+                            nullptr);
+    } else if (grouped) {
       RowGroups g1{offsets, E, a.hidden * a.d, a.hidden};
       RowGroups g2{offsets, E, a.d * a.hidden, a.d};
       split_planes(a.x, row_token, entries, a.d, planes1, entries, kp1, planes);

@@ -32,7 +32,22 @@ int64_t gemm_k_pad(int64_t k);
 int64_t f16f8_k_pad(int64_t k);
 size_t f16f8_bytes(int64_t m, int64_t k);
 bool f16f8_supported(int64_t k, const int8_t* codes);
-void split_f16f8(const float* x, int64_t m, int64_t k, void* buf);
+// Row r of the split comes from row gather[r] of x (nullptr: row r).  With
+// `bound` (f16f8_bound_params' two floats on the device), exps2[r] receives
+// the exponent of a split of a Dense output computed from row r, bounded by
+// sum_k |x| * bound[0] + bound[1].
+void split_f16f8(const float* x, int64_t m, int64_t k, void* buf, const int* gather = nullptr,
+                 const float* bound = nullptr, int* exps2 = nullptr);
+// The two constants of that bound for codes with scales w_scale (ns values)
+// and bias (nb values or nullptr) under the epilogue's activation.
+void f16f8_bound_params(const float* w_scale, int64_t ns, const float* bias, int64_t nb,
+                        const Epilogue& ep, float* out);
+// Row-grouped GEMM on split activations (256 x 256 tiles); with `out_split`
+// the activated (m, n) output is written as the next GEMM's split (n a
+// multiple of 64) with the exponents already in out_split's exponent array.
+void gemm_w8_f16f8_grouped(const void* buf, int64_t m, int64_t k, const int8_t* codes,
+                           const float* w_scale, int64_t n, const float* bias,
+                           const RowGroups& grp, const Epilogue& ep, float* y, void* out_split);
 // act(x @ (codes * w_scale).T + bias) from split_f16f8's buffer; the
 // epilogue's fake-quantization is not applied (gemm_epilogue(ep, false)).
 void gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes,
