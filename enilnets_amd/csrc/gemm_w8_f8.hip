@@ -51,8 +51,10 @@ __device__ __forceinline__ int row_exponent(float amax) {
 
 // Four activations -> their fp16 high parts (two dwords) and e4m3 low parts
 // (one dword), after scaling by 2^e.
-__device__ __forceinline__ void split4_f16f8(float4 v, int e, uint2& hi, uint32_t& lo) {
+__device__ __forceinline__ void split4_f16f8(float4 v, int e, uint2& hi, uint32_t& lo,
+                                             float& sumsq) {
   const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+  sumsq += (a[0] * a[0] + a[1] * a[1]) + (a[2] * a[2] + a[3] * a[3]);
   _Float16 h[4];
   float r[4];
 #pragma unroll
@@ -83,9 +85,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 // aligned, k <= 1024 * V) stays in registers between its maximum and its
 // split; otherwise it is read twice with scalar loads.  Row r of the split
 // comes from row gather[r] of x (gather == nullptr: row r).  With `bound`,
-// the row also gets a second exponent, exps2[r], for a GEMM output computed
-// from it: that of the bound sum_k |x| * bound[0] + bound[1] on every output
-// of the row (f16f8_bound_params).
+// the row also gets a second exponent, exps2[r], for a Dense output computed
+// from it: that of ||x||_2 * bound[0] + bound[1], a bound on every output of
+// the row (f16f8_bound_params).  ||x||_2 comes from the scaled values
+// x * 2^e (no overflow: |x * 2^e| < 2^15).
 template <int V, bool REGS>
 __global__ __launch_bounds__(256) void split_f16f8_kernel(const float* __restrict__ x,
                                                           const int* __restrict__ gather,
@@ -95,49 +98,31 @@ __global__ __launch_bounds__(256) void split_f16f8_kernel(const float* __restric
                                                           int* __restrict__ exps,
                                                           const float* __restrict__ bound,
                                                           int* __restrict__ exps2) {
-  __shared__ float red[4], red_sum[4];
+  __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const float* xr = x + (gather ? int64_t(gather[row]) : row) * k;
   const int tid = threadIdx.x;
   float amax = 0.0f;  // fmaxf skips NaN
-  float l1 = 0.0f;
   float4 v[REGS ? V : 1];
   if constexpr (REGS) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int64_t c = (int64_t(j) * 256 + tid) * 4;
       v[j] = c < k ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float ax = fabsf(v[j].x), ay = fabsf(v[j].y), az = fabsf(v[j].z), aw = fabsf(v[j].w);
-      amax = fmaxf(amax, fmaxf(fmaxf(ax, ay), fmaxf(az, aw)));
-      if (bound) l1 += (ax + ay) + (az + aw);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
     }
   } else {
-    for (int64_t c = tid; c < k; c += 256) {
-      const float ax = fabsf(xr[c]);
-      amax = fmaxf(amax, ax);
-      if (bound) l1 += ax;
-    }
+    for (int64_t c = tid; c < k; c += 256) amax = fmaxf(amax, fabsf(xr[c]));
   }
   amax = wave_max(amax);
-  if (bound) l1 = wave_sum(l1);
-  if ((tid & 63) == 0) {
-    red[tid >> 6] = amax;
-    red_sum[tid >> 6] = l1;
-  }
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const int e = row_exponent(amax);
-  if (tid == 0) {
-    exps[row] = e;
-    if (bound) {
-      // a float sum of |x| is within k * 2^-24 of the exact one; the bound
-      // is only an upper limit for the output's scale, so the margin is ample
-      const float total = ((red_sum[0] + red_sum[1]) + (red_sum[2] + red_sum[3])) * 1.01f;
-      exps2[row] = row_exponent(total * bound[0] + bound[1]);
-    }
-  }
+  if (tid == 0) exps[row] = e;
   uint16_t* hr = hi + row * kp;
   uint8_t* lr = lo + row * kp;
+  float sumsq = 0.0f;
   if constexpr (REGS) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
@@ -145,7 +130,7 @@ __global__ __launch_bounds__(256) void split_f16f8_kernel(const float* __restric
       if (c < kp) {
         uint2 h;
         uint32_t l;
-        split4_f16f8(v[j], e, h, l);
+        split4_f16f8(v[j], e, h, l, sumsq);
         *reinterpret_cast<uint2*>(hr + c) = h;
         *reinterpret_cast<uint32_t*>(lr + c) = l;
       }
@@ -159,28 +144,70 @@ __global__ __launch_bounds__(256) void split_f16f8_kernel(const float* __restric
       t.w = c + 3 < k ? xr[c + 3] : 0.0f;
       uint2 h;
       uint32_t l;
-      split4_f16f8(t, e, h, l);
+      split4_f16f8(t, e, h, l, sumsq);
       *reinterpret_cast<uint2*>(hr + c) = h;
       *reinterpret_cast<uint32_t*>(lr + c) = l;
     }
   }
+  if (bound) {
+    sumsq = wave_sum(sumsq);
+    __syncthreads();  // red[] is reused
+    if ((tid & 63) == 0) red[tid >> 6] = sumsq;
+    __syncthreads();
+    if (tid == 0) {
+      // a float sum of squares is within k * 2^-24 of the exact one; the
+      // bound is only an upper limit for the output's scale, so a 1% margin
+      // is ample
+      const float l2 = ldexpf(sqrtf((red[0] + red[1]) + (red[2] + red[3])), -e) * 1.01f;
+      exps2[row] = row_exponent(l2 * bound[0] + bound[1]);
+    }
+  }
 }
 
-// The constants of split_f16f8_kernel's output bound for a Dense
-// act(scale[n] * sum_k x_k q_nk + bias[n]) with |q| <= 127:
-//   |out| <= c * (127 * max scale * sum_k |x_k| + max |bias|) + 2 c,
-//   c = 1.07 * max(1, |alpha|),
-// which covers every activation of the epilogue (|act(z)| <= |z| for linear,
-// relu, gelu, swish, mish; leaky slopes; elu / selu, sigmoid, tanh and
-// softplus add at most 1.76).  One workgroup.
-__global__ __launch_bounds__(256) void f16f8_bound_kernel(const float* __restrict__ scale,
-                                                          int64_t ns,
+// Per-output-channel norms of a Dense's codes for split_f16f8_kernel's
+// bound: |sum_k x_k q_nk| <= ||x||_2 * ||q_n||_2 (Cauchy-Schwarz).  Each wave
+// takes rows of `codes` (rows, k) in turn (k % 16 == 0, 16-byte aligned) and
+// the workgroup writes max_n scale[n] * ||q_n||_2 over its rows to part[].
+__global__ __launch_bounds__(256) void code_norm_kernel(const int8_t* __restrict__ codes,
+                                                        int64_t rows, int64_t k,
+                                                        const float* __restrict__ scale,
+                                                        float* __restrict__ part) {
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float best = 0.0f;
+  for (int64_t r = int64_t(blockIdx.x) * 4 + wave; r < rows; r += int64_t(gridDim.x) * 4) {
+    const int8_t* cr = codes + r * k;
+    int acc = 0;
+    for (int64_t c = int64_t(lane) * 16; c < k; c += 1024) {
+      const int4 q = *reinterpret_cast<const int4*>(cr + c);
+      acc = __builtin_amdgcn_sdot4(q.x, q.x, acc, false);
+      acc = __builtin_amdgcn_sdot4(q.y, q.y, acc, false);
+      acc = __builtin_amdgcn_sdot4(q.z, q.z, acc, false);
+      acc = __builtin_amdgcn_sdot4(q.w, q.w, acc, false);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    best = fmaxf(best, fabsf(scale[r]) * sqrtf(float(acc)));
+  }
+  if (lane == 0) red[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// The two constants of the bound |act(z_n)| <= bound[0] * ||x||_2 + bound[1]
+// for z_n = scale[n] * sum_k x_k q_nk + bias[n]:
+//   bound[0] = c * max_n scale[n] * ||q_n||_2,  bound[1] = c * max |bias| + d,
+// with |act(z)| <= c |z| + d for the epilogue's activation: c = 1 for linear,
+// relu, gelu, swish, mish and tanh, max(1, |alpha|) for the leaky slopes and
+// elu, 1.76 for selu; d = 1 for sigmoid (c = 0) and ln 2 for softplus; each
+// widened by 1%.  One workgroup.
+__global__ __launch_bounds__(256) void f16f8_bound_kernel(const float* __restrict__ part, int parts,
                                                           const float* __restrict__ bias,
-                                                          int64_t nb, float c,
+                                                          int64_t nb, float c, float d,
                                                           float* __restrict__ out) {
   __shared__ float red_s[4], red_b[4];
   float ms = 0.0f, mb = 0.0f;
-  for (int64_t i = threadIdx.x; i < ns; i += 256) ms = fmaxf(ms, fabsf(scale[i]));
+  for (int i = threadIdx.x; i < parts; i += 256) ms = fmaxf(ms, part[i]);
   for (int64_t i = threadIdx.x; i < nb; i += 256) mb = fmaxf(mb, fabsf(bias[i]));
   ms = wave_max(ms);
   mb = wave_max(mb);
@@ -192,8 +219,8 @@ __global__ __launch_bounds__(256) void f16f8_bound_kernel(const float* __restric
   if (threadIdx.x == 0) {
     ms = fmaxf(fmaxf(red_s[0], red_s[1]), fmaxf(red_s[2], red_s[3]));
     mb = fmaxf(fmaxf(red_b[0], red_b[1]), fmaxf(red_b[2], red_b[3]));
-    out[0] = c * 127.0f * ms;
-    out[1] = c * (mb + 2.0f);
+    out[0] = c * ms * 1.01f;
+    out[1] = (c * mb + d) * 1.01f;
   }
 }
 
@@ -621,10 +648,23 @@ void split_f16f8(const float* x, int64_t m, int64_t k, void* buf, const int* gat
   check_launch("split_f16f8_kernel");
 }
 
-void f16f8_bound_params(const float* w_scale, int64_t ns, const float* bias, int64_t nb,
-                        const Epilogue& ep, float* out) {
-  const float c = 1.07f * fmaxf(1.0f, fabsf(ep.alpha));
-  f16f8_bound_kernel<<<1, 256, 0, stream()>>>(w_scale, ns, bias, bias ? nb : 0, c, out);
+void f16f8_bound_params(const int8_t* codes, int64_t rows, int64_t k, const float* w_scale,
+                        const float* bias, const Epilogue& ep, float* out) {
+  ENQ_REQUIRE(f16f8_supported(k, codes), "code norms need K a multiple of 16 and aligned codes");
+  float c = 1.0f, d = 0.0f;
+  switch (ep.activation) {
+    case ENQ_ACT_LEAKYRELU:
+    case ENQ_ACT_ELU: c = fmaxf(1.0f, fabsf(ep.alpha)); break;
+    case ENQ_ACT_SELU: c = 1.76f; break;
+    case ENQ_ACT_SIGMOID: c = 0.0f; d = 1.0f; break;
+    case ENQ_ACT_SOFTPLUS: d = 0.7f; break;
+    default: break;
+  }
+  float* part = out + 2;
+  const int parts = int(std::min<int64_t>(kBoundParts, ceil_div(rows, 4)));
+  code_norm_kernel<<<unsigned(parts), 256, 0, stream()>>>(codes, rows, k, w_scale, part);
+  check_launch("code_norm_kernel");
+  f16f8_bound_kernel<<<1, 256, 0, stream()>>>(part, parts, bias, bias ? rows : 0, c, d, out);
   check_launch("f16f8_bound_kernel");
 }
 

@@ -368,8 +368,12 @@ void moe_w8(const MoeArgs& a) {
   const int64_t kp1 = gemm_k_pad(a.d), kp2 = gemm_k_pad(a.hidden);
   // fp32-accurate expert GEMMs on the fp16 / e4m3 split: the gathered token
   // rows are split once, the first GEMM writes the hidden activations as the
-  // second's split (their row exponents come from a bound computed in the
-  // first split), and neither GEMM reads bf16 planes
+  // second's split, and neither GEMM reads bf16 planes.  The hidden rows'
+  // exponents come from a bound computed in the first split,
+  // ||x||_2 * max_n scale_n ||q_n||_2 (+ bias, widened for the activation),
+  // which stays within a few powers of two of the rows' true maxima, so the
+  // high parts stay inside fp16's range and the low parts of the outputs
+  // that matter inside e4m3's normal range
   const bool split8 = grouped && planes == 2 && f16f8_supported(a.d, a.w1) &&
                       f16f8_supported(a.hidden, a.w2) && a.hidden % 64 == 0 &&
                       a.ep.aq == ENQ_AQ_NONE && a.ep.activation != ENQ_ACT_SOFTMAX;
@@ -394,7 +398,7 @@ void moe_w8(const MoeArgs& a) {
     float* yg = c.take<float>(entries * a.d);
     char* split1 = split8 ? c.take<char>(int64_t(f16f8_bytes(entries, a.d))) : nullptr;
     char* split2 = split8 ? c.take<char>(int64_t(f16f8_bytes(entries, a.hidden))) : nullptr;
-    float* bound = split8 ? c.take<float>(2) : nullptr;
+    float* bound = split8 ? c.take<float>(2 + kBoundParts) : nullptr;
     use(c.used(), logits, probs, chosen, gates, hist, offsets, row_token, entry_pos, terms,
         planes1, xg, h, planes2, yg, split1, split2, bound);
   };
@@ -436,7 +440,7 @@ void moe_w8(const MoeArgs& a) {
       RowGroups g2{offsets, E, a.d * a.hidden, a.d};
       // the second split's exponents sit after its two planes
       int* exps2 = reinterpret_cast<int*>(split2 + 3 * entries * f16f8_k_pad(a.hidden));
-      f16f8_bound_params(a.s1, E * a.hidden, a.b1, E * a.hidden, a.ep, bound);
+      f16f8_bound_params(a.w1, E * a.hidden, a.d, a.s1, a.b1, a.ep, bound);
       split_f16f8(a.x, entries, a.d, split1, row_token, bound, exps2);
       gemm_w8_f16f8_grouped(split1, entries, a.d, a.w1, a.s1, a.hidden, a.b1, g1, a.ep, nullptr,
                             split2);

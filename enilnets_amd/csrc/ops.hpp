@@ -35,13 +35,15 @@ bool f16f8_supported(int64_t k, const int8_t* codes);
 // Row r of the split comes from row gather[r] of x (nullptr: row r).  With
 // `bound` (f16f8_bound_params' two floats on the device), exps2[r] receives
 // the exponent of a split of a Dense output computed from row r, bounded by
-// sum_k |x| * bound[0] + bound[1].
+// ||x_r||_2 * bound[0] + bound[1].
 void split_f16f8(const float* x, int64_t m, int64_t k, void* buf, const int* gather = nullptr,
                  const float* bound = nullptr, int* exps2 = nullptr);
-// The two constants of that bound for codes with scales w_scale (ns values)
-// and bias (nb values or nullptr) under the epilogue's activation.
-void f16f8_bound_params(const float* w_scale, int64_t ns, const float* bias, int64_t nb,
-                        const Epilogue& ep, float* out);
+// The two constants of that bound for the Dense with codes (rows, k), scales
+// w_scale and bias (rows values or nullptr) under the epilogue's activation,
+// written to out[0..1]; out[2 .. 2 + kBoundParts) is scratch.
+constexpr int kBoundParts = 1024;
+void f16f8_bound_params(const int8_t* codes, int64_t rows, int64_t k, const float* w_scale,
+                        const float* bias, const Epilogue& ep, float* out);
 // Row-grouped GEMM on split activations (256 x 256 tiles); with `out_split`
 // the activated (m, n) output is written as the next GEMM's split (n a
 // multiple of 64) with the exponents already in out_split's exponent array.

@@ -154,6 +154,54 @@ def test_moe_empty_experts(gpu):
     assert np.all(row_rel_err(out.numpy(), want) <= 1e-4)
 
 
+@pytest.mark.parametrize("activation", ["gelu", "relu", "sigmoid", "selu"])
+def test_moe_split_rows_of_every_kind(gpu, activation):
+    # the fp32 layer's fp16 / e4m3 path (hidden a multiple of 64): token rows
+    # of very different scales and shapes, and expert weights with one
+    # 50-sigma entry per output channel (per-row scales), all within the
+    # Dense bound.  The hidden rows' exponents come from a bound on them, so
+    # these are the rows where a loose bound would lose the low parts.
+    print(f"[case] moe split rows activation={activation}", flush=True)
+    rng = np.random.default_rng(17)
+    experts, d, hidden, tokens = 4, 128, 256, 600
+    m = Model()
+    w1 = (rng.standard_normal((experts, hidden, d)) * 0.02).astype(np.float32)
+    w2 = (rng.standard_normal((experts, d, hidden)) * 0.02).astype(np.float32)
+    for w in (w1, w2):
+        e_i, n_i = np.meshgrid(np.arange(w.shape[0]), np.arange(w.shape[1]), indexing="ij")
+        w[e_i, n_i, rng.integers(0, w.shape[2], w.shape[:2])] = 1.0
+    wr = (rng.standard_normal((experts, d)) / np.sqrt(d)).astype(np.float32)
+    b1 = (rng.standard_normal((experts, hidden)) * 0.01).astype(np.float32)
+    b2 = (rng.standard_normal((experts, d)) * 0.01).astype(np.float32)
+    m.add_moe(w1, w2, wr, top_k=2, activation=activation, b1=b1, b2=b2)
+    L = m.layers[0]
+    L["quant"] = {}
+    for name in ("W1", "W2"):
+        fq, sc = [], []
+        for e in range(experts):
+            f, s, _ = oracle.quantize_tensor(L[name][e], 8, per_channel=True)
+            fq.append(f)
+            sc.append(s)
+        L[name] = np.stack(fq)
+        L["quant"][name] = {"bits": 8, "scheme": "symmetric", "scale": np.stack(sc),
+                            "zero_point": np.zeros_like(np.stack(sc))}
+    x = rng.standard_normal((tokens, d))
+    kinds = np.arange(tokens) % 6
+    x[kinds == 1] *= 1e-6
+    x[kinds == 2] *= 1e-30
+    x[kinds == 3] = rng.standard_cauchy((int(np.sum(kinds == 3)), d))
+    x[kinds == 4] *= np.exp(rng.normal(0.0, 3.0, (int(np.sum(kinds == 4)), d)))
+    x[kinds == 5, :4] *= 1000.0
+    x = x.astype(np.float32)
+    logits = rng.standard_normal((tokens, experts)).astype(np.float32)
+    out, _ = moe_forward(DeviceArray.from_numpy(x), L,
+                         router_logits=DeviceArray.from_numpy(logits))
+    probs = softmax32(logits)
+    want = oracle.moe_forward(x.astype(np.float64), L, probs=probs.astype(np.float64))
+    err = row_rel_err(out.numpy(), want)
+    assert np.all(err <= 1e-4), f"max row error {err.max():.3e} (row kind {kinds[np.argmax(err)]})"
+
+
 @pytest.mark.parametrize("d,hidden", [(64, 256), (48, 80)])
 def test_moe_layer_bf16(gpu, d, hidden):
     # the bf16 variant (one plane per activation); hidden 256 has the first
