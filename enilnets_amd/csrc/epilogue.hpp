@@ -35,11 +35,17 @@ __device__ __forceinline__ float fake_quant(float v, const Epilogue& e) {
   return __fmul_rn(c - zp, s);
 }
 
-// activations.py GELU (tanh form), one element.
+// activations.py GELU (tanh form), one element:
+//   0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3),
+// the same function with one exponential and one reciprocal in place of tanh
+// (a third of the instructions in the GEMM epilogues).  exp2 of a rounded
+// argument is within |2u| 2^-24 relative; where that exceeds 2e-6 (|2u| > 33)
+// the output is below 1e-13.  The reciprocal form has no cancellation in
+// 1 + tanh(u) for negative x.
 __device__ __forceinline__ float gelu(float x) {
-  const float c = 0.7978845608028654f;  // sqrt(2 / pi)
-  float inner = c * (x + 0.044715f * (x * x * x));
-  return 0.5f * x * (1.0f + tanhf(inner));
+  const float c2 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
+  const float t = c2 * (x + 0.044715f * (x * x * x));
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
 // activations.py:21-41, one element.  relu keeps -0.0 and NaN as np.maximum

@@ -292,7 +292,8 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
                        const int* __restrict__ xe, int64_t kp, const int8_t* __restrict__ w,
                        const float* __restrict__ scale, const float* __restrict__ bias,
                        int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n, RowGroups grp,
-                       Epilogue ep, float* __restrict__ y, float* __restrict__ z, F8Out yo) {
+                       Epilogue ep, float* __restrict__ y, float* __restrict__ z, F8Out yo,
+                       int ksplit) {
   constexpr int BM = C::BM, BN = C::BN, WN = C::WN, AHEAD = C::AHEAD, BK = C::BK;
   constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN;
   constexpr int A_PW = C::A_PW, B_PW = C::B_PW, DPW = C::DPW;
@@ -300,8 +301,13 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
   char* lds = reinterpret_cast<char*>(lds_raw);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
+  // split K (ksplit > 1): workgroup b takes K part b / tiles of tile
+  // b % tiles, writes that part's sums (scaled, bias only in part 0, no
+  // activation) to y + part * m * n, and the caller adds the parts
+  const int tiles = tiles_m * tiles_n;
+  const int part = int(blockIdx.x) / tiles;
   int tm, tn;
-  xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
+  xcd_tile(int(blockIdx.x) - part * tiles, tiles_m, tiles_n, 4, tm, tn);
   int64_t m0 = int64_t(tm) * BM, m_end = m;
   const int64_t n0 = int64_t(tn) * BN;
   if (grp.offsets) {
@@ -347,12 +353,16 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
     b_koff[j] = 16 * swz32(r, lane & 1);
     b_voff[j] = uint32_t(g * k + b_koff[j]);
   }
-  const int ktiles = int(kp / BK);  // even: kp is a multiple of 64
+  // this part's stages: an even number (kp is a multiple of 64), at least two
+  const int kt_all = int(kp / BK), kt_part = (kt_all / ksplit + 1) & ~1;
+  const int t0 = part * kt_part;
+  const int ktiles = min(kt_part, kt_all - t0);
+  const int64_t k_rem = k - int64_t(t0) * BK;  // codes from this part's first column
   const void* zero = g_zero16;
   const uint32_t lds0 = lds_addr(lds);
-  const char* xh_b = reinterpret_cast<const char*>(xh);
-  const char* xl_b = reinterpret_cast<const char*>(xl);
-  const char* w_b = reinterpret_cast<const char*>(w);
+  const char* xh_b = reinterpret_cast<const char*>(xh) + int64_t(t0) * (2 * BK);
+  const char* xl_b = reinterpret_cast<const char*>(xl) + int64_t(t0) * BK;
+  const char* w_b = reinterpret_cast<const char*>(w) + int64_t(t0) * BK;
   // block j (< A_PW: A, else codes) of this wave's group G(s): A tile s and
   // code tile s + 1.  Tiles past the end of K reload the last one into a
   // slot no one reads again (uniform wait counts).
@@ -368,7 +378,7 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
     const uint32_t dst = lds0 + C::B_RING + (s % C::B_SLOTS) * C::B_BYTES + blk * 1024;
     if constexpr (KTAIL) {
       // 16-byte chunks past k read the zero block
-      const bool live = sc * BK + b_koff[j] < k;
+      const bool live = sc * BK + b_koff[j] < k_rem;
       dma16(live ? static_cast<const void*>(w_b + b_voff[j] + sc * BK) : zero, dst);
     } else {
       dma16_s(b_voff[j], w_b + sc * BK, dst);
@@ -554,13 +564,13 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
         const int64_t col = n0 + wn * TN + j * 32 + lrow;
         if (col >= n) continue;
         const float s = scale[col];
-        const float b = bias ? bias[col] : 0.f;
+        const float b = bias && part == 0 ? bias[col] : 0.f;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int64_t row = row0 + 8 * (e / 4) + (e % 4);
           if (row < m_end) {
             float v = ldexpf(acc[i][j][e], ex[e]) * s;
-            if (bias) v = v + b;
+            if (bias && part == 0) v = v + b;
             if constexpr (YF8) {
               // the next GEMM's split of this output (split4_f16f8's arithmetic)
               const float a = ldexpf(act(v), eo[e]);
@@ -568,6 +578,8 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
               yo.hi[row * yo.ld + col] = __builtin_bit_cast(uint16_t, h);
               yo.lo[row * yo.ld + col] =
                   uint8_t(__builtin_amdgcn_cvt_pk_fp8_f32(a - static_cast<float>(h), 0.0f, 0, false));
+            } else if (ksplit > 1) {
+              y[int64_t(part) * m * n + row * n + col] = v;
             } else {
               if (z) z[row * n + col] = v;
               y[row * n + col] = act(v);
@@ -583,11 +595,13 @@ template <class C>
 void launch_w8_f8(const uint16_t* xh, const uint8_t* xl, const int* xe, int64_t kp,
                   const int8_t* w, const float* scale, const float* bias, int64_t m, int64_t n,
                   int64_t k, const Epilogue& ep, float* y, float* z,
-                  const RowGroups& grp = RowGroups{}, const F8Out& yo = F8Out{}) {
+                  const RowGroups& grp = RowGroups{}, const F8Out& yo = F8Out{}, int ksplit = 1) {
   // grouped rows: every group may end in a partial tile
   const int64_t tiles_m = ceil_div(m, C::BM) + (grp.offsets ? grp.groups : 0);
   const int64_t tiles_n = ceil_div(n, C::BN);
-  ENQ_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "problem too large");
+  ENQ_REQUIRE(tiles_m * tiles_n * ksplit <= 0x7fffffff, "problem too large");
+  ENQ_REQUIRE(ksplit == 1 || (yo.hi == nullptr && z == nullptr && (kp / C::BK) / ksplit >= 2),
+              "split K: fp32 partial sums of at least two stages each");
   const size_t lds_bytes = size_t(C::LDS_BYTES);
   static bool attr_set = false;
   if (!attr_set) {
@@ -601,8 +615,9 @@ void launch_w8_f8(const uint16_t* xh, const uint8_t* xl, const int* xe, int64_t 
   auto kernel = (k % C::BK == 0) ? w8_f8_ring_kernel<C, false> : w8_f8_ring_kernel<C, true>;
   if (yo.hi)
     kernel = (k % C::BK == 0) ? w8_f8_ring_kernel<C, false, true> : w8_f8_ring_kernel<C, true, true>;
-  kernel<<<unsigned(tiles_m * tiles_n), C::NT, lds_bytes, stream()>>>(
-      xh, xl, xe, kp, w, scale, bias, m, n, k, int(tiles_m), int(tiles_n), grp, ep, y, z, yo);
+  kernel<<<unsigned(tiles_m * tiles_n * ksplit), C::NT, lds_bytes, stream()>>>(
+      xh, xl, xe, kp, w, scale, bias, m, n, k, int(tiles_m), int(tiles_n), grp, ep, y, z, yo,
+      ksplit);
   check_launch("w8_f8_ring_kernel");
 }
 
@@ -688,7 +703,8 @@ void gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes,
 
 void gemm_w8_f16f8_grouped(const void* buf, int64_t m, int64_t k, const int8_t* codes,
                            const float* w_scale, int64_t n, const float* bias,
-                           const RowGroups& grp, const Epilogue& ep, float* y, void* out_split) {
+                           const RowGroups& grp, const Epilogue& ep, float* y, void* out_split,
+                           int ksplit) {
   ENQ_REQUIRE(f16f8_supported(k, codes),
               "the fp16/fp8 split GEMM needs K a multiple of 16 and 16-byte aligned codes");
   ENQ_REQUIRE(ep.aq == ENQ_AQ_NONE && ep.activation != ENQ_ACT_SOFTMAX,
@@ -703,8 +719,9 @@ void gemm_w8_f16f8_grouped(const void* buf, int64_t m, int64_t k, const int8_t* 
     const F16F8View o = f16f8_view(out_split, m, n);
     yo = F8Out{o.hi, o.lo, o.exps, n};
   }
+  ENQ_REQUIRE(ksplit == 1 || ep.activation == ENQ_ACT_LINEAR, "split K needs a linear epilogue");
   launch_w8_f8<F8Big>(v.hi, v.lo, v.exps, kp, codes, w_scale, bias, m, n, k, ep, y, nullptr, grp,
-                      yo);
+                      yo, ksplit);
 }
 
 }  // namespace enq

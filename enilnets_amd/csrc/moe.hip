@@ -212,6 +212,7 @@ __global__ __launch_bounds__(kSortBlock) void moe_place_kernel(const int* __rest
 // out[t, c] = sum over t's slots in ascending expert order of gate * y.
 template <int V>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ yg,
+                                                          const float* __restrict__ yg2,
                                                           const int* __restrict__ chosen,
                                                           const float* __restrict__ gates,
                                                           const int* __restrict__ entry_pos,
@@ -238,7 +239,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     }
     last = best;
     const float g = gates[t * top_k + slot];
-    const float* y = yg + int64_t(entry_pos[t * top_k + slot]) * d + c0;
+    const int64_t at = int64_t(entry_pos[t * top_k + slot]) * d + c0;
+    const float* y = yg + at;
     float q[V];
     if constexpr (V == 4) {
       const float4 w = *reinterpret_cast<const float4*>(y);
@@ -246,9 +248,17 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
       q[1] = w.y;
       q[2] = w.z;
       q[3] = w.w;
+      if (yg2) {
+        // the second K part of the expert GEMM
+        const float4 w2 = *reinterpret_cast<const float4*>(yg2 + at);
+        q[0] = q[0] + w2.x;
+        q[1] = q[1] + w2.y;
+        q[2] = q[2] + w2.z;
+        q[3] = q[3] + w2.w;
+      }
     } else {
 #pragma unroll
-      for (int v = 0; v < V; ++v) q[v] = y[v];
+      for (int v = 0; v < V; ++v) q[v] = yg2 ? y[v] + yg2[at + v] : y[v];
     }
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[v] = acc[v] + g * q[v];
@@ -395,7 +405,7 @@ void moe_w8(const MoeArgs& a) {
     float* xg = grouped ? nullptr : c.take<float>(entries * a.d);
     float* h = split8 ? nullptr : c.take<float>(entries * a.hidden);
     uint16_t* planes2 = pl ? c.take<uint16_t>(int64_t(planes) * entries * kp2) : nullptr;
-    float* yg = c.take<float>(entries * a.d);
+    float* yg = c.take<float>(entries * a.d * (split8 ? 2 : 1));
     char* split1 = split8 ? c.take<char>(int64_t(f16f8_bytes(entries, a.d))) : nullptr;
     char* split2 = split8 ? c.take<char>(int64_t(f16f8_bytes(entries, a.hidden))) : nullptr;
     float* bound = split8 ? c.take<float>(2 + kBoundParts) : nullptr;
@@ -435,6 +445,7 @@ void moe_w8(const MoeArgs& a) {
     check_launch("moe_place_kernel");
 
     const Epilogue lin{ENQ_ACT_LINEAR, 0.0f, 0.0f};
+    const float* yg2 = nullptr;  // the second K part of the expert outputs, if split
     if (split8) {
       RowGroups g1{offsets, E, a.hidden * a.d, a.hidden};
       RowGroups g2{offsets, E, a.d * a.hidden, a.d};
@@ -444,8 +455,15 @@ void moe_w8(const MoeArgs& a) {
       split_f16f8(a.x, entries, a.d, split1, row_token, bound, exps2);
       gemm_w8_f16f8_grouped(split1, entries, a.d, a.w1, a.s1, a.hidden, a.b1, g1, a.ep, nullptr,
                             split2);
+      // K of the second GEMM in two parts, added in the combine: its tiles
+      // (ceil(entries / 256) + E tile rows x d / 256) slightly exceed one
+      // round of the device at configs[4], where a second round held 8 tiles
+      const int64_t t2 = (ceil_div(entries, 256) + E) * ceil_div(a.d, 256);
+      const int64_t cus = device_cu_count();
+      const bool halves = a.hidden >= 256 && ceil_div(2 * t2, cus) < 2 * ceil_div(t2, cus);
       gemm_w8_f16f8_grouped(split2, entries, a.hidden, a.w2, a.s2, a.d, a.b2, g2, lin, yg,
-                            nullptr);
+                            nullptr, halves ? 2 : 1);
+      if (halves) yg2 = yg + entries * a.d;
     } else if (grouped) {
       RowGroups g1{offsets, E, a.hidden * a.d, a.hidden};
       RowGroups g2{offsets, E, a.d * a.hidden, a.d};
@@ -485,10 +503,10 @@ void moe_w8(const MoeArgs& a) {
     }
     if (a.d % 4 == 0 && aligned(a.out, 16))
       moe_combine_kernel<4><<<blocks_for(a.tokens * (a.d / 4)), 256, 0, s>>>(
-          yg, chosen, gates, entry_pos, a.tokens, a.d, a.top_k, a.out);
+          yg, yg2, chosen, gates, entry_pos, a.tokens, a.d, a.top_k, a.out);
     else
       moe_combine_kernel<1><<<blocks_for(a.tokens * a.d), 256, 0, s>>>(
-          yg, chosen, gates, entry_pos, a.tokens, a.d, a.top_k, a.out);
+          yg, yg2, chosen, gates, entry_pos, a.tokens, a.d, a.top_k, a.out);
     check_launch("moe_combine_kernel");
     if (a.top_idx)
       ENQ_HIP(hipMemcpyAsync(a.top_idx, chosen, sizeof(int) * entries, hipMemcpyDeviceToDevice,

@@ -47,9 +47,12 @@ void f16f8_bound_params(const int8_t* codes, int64_t rows, int64_t k, const floa
 // Row-grouped GEMM on split activations (256 x 256 tiles); with `out_split`
 // the activated (m, n) output is written as the next GEMM's split (n a
 // multiple of 64) with the exponents already in out_split's exponent array.
+// ksplit > 1 (linear epilogue, y output): K in that many parts, part p's
+// sums (bias in part 0 only) at y + p * m * n, for the caller to add.
 void gemm_w8_f16f8_grouped(const void* buf, int64_t m, int64_t k, const int8_t* codes,
                            const float* w_scale, int64_t n, const float* bias,
-                           const RowGroups& grp, const Epilogue& ep, float* y, void* out_split);
+                           const RowGroups& grp, const Epilogue& ep, float* y, void* out_split,
+                           int ksplit = 1);
 // act(x @ (codes * w_scale).T + bias) from split_f16f8's buffer; the
 // epilogue's fake-quantization is not applied (gemm_epilogue(ep, false)).
 void gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes,
