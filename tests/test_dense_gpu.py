@@ -195,8 +195,8 @@ def test_split_f16f8_layout(gpu, m, k):
 
 
 @pytest.mark.parametrize("m,k,n", [(4096, 1024, 4096), (4100, 1040, 4100), (4097, 2048, 4095),
-                                   (1024, 2304, 4096), (300, 784, 1024), (129, 48, 260),
-                                   (65, 64, 32)])
+                                   (4096, 1024, 3072), (1024, 2304, 4096), (300, 784, 1024),
+                                   (129, 48, 260), (65, 64, 32)])
 def test_dense_w8_split(gpu, m, k, n):
     # the fp16 / e4m3 split GEMM within the fp32 bound on rows of every kind,
     # and, where dense_w8 takes it (tiles that fill the device, or more than
