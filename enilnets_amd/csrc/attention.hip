@@ -9,7 +9,9 @@
 // one query's column and the softmax statistics are per lane; masks,
 // running max and the rescale follow; then O^T += V^T . P^T reuses the score
 // registers directly as the B operand.  Everything is fp32: products are
-// exact fp32 products, sums fp32.
+// exact fp32 products, sums fp32.  attention_bf16_kernel (head_dim 32, 64,
+// 128) keeps that layout on the bf16 matrix cores: every operand split into
+// three bf16 parts, six part products per product.
 #include <algorithm>
 #include <cmath>
 
@@ -391,6 +393,329 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
   }
 }
 
+// fp32 x -> bf16 h + m + l with x - h - m - l within about 2^-27 |x| (each
+// difference is exact in fp32, each part nearest even).
+__device__ __forceinline__ void split3_bf16(float x, uint16_t& h, uint16_t& m, uint16_t& l) {
+  h = bf16_bits_rne(x);
+  const float r = x - bf16_to_float(h);
+  m = bf16_bits_rne(r);
+  l = bf16_bits_rne(r - bf16_to_float(m));
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// The same for two values at once (one v_cvt_pk_bf16_f32 per part), each
+// part returned as a packed pair, a in the low half.
+__device__ __forceinline__ void split3_bf16x2(float a, float b, uint32_t& h, uint32_t& m,
+                                              uint32_t& l) {
+  h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+  const float ra = a - __uint_as_float(h << 16), rb = b - __uint_as_float(h & 0xffff0000u);
+  m = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{ra, rb}, bf16x2));
+  const float sa = ra - __uint_as_float(m << 16), sb = rb - __uint_as_float(m & 0xffff0000u);
+  l = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{sa, sb}, bf16x2));
+}
+
+// Eight values -> their three bf16 parts as MFMA operands.
+__device__ __forceinline__ void split3_bf16x8(const float (&x)[8], bf16x8& h, bf16x8& m,
+                                              bf16x8& l) {
+  uint32_t ph[4], pm[4], pl[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) split3_bf16x2(x[2 * i], x[2 * i + 1], ph[i], pm[i], pl[i]);
+  h = __builtin_bit_cast(bf16x8, make_uint4(ph[0], ph[1], ph[2], ph[3]));
+  m = __builtin_bit_cast(bf16x8, make_uint4(pm[0], pm[1], pm[2], pm[3]));
+  l = __builtin_bit_cast(bf16x8, make_uint4(pl[0], pl[1], pl[2], pl[3]));
+}
+
+// a . b to fp32 accuracy from three-part operands: the six products whose
+// parts are above 2^-18 of the whole, smallest first into the accumulator.
+__device__ __forceinline__ floatx4 mfma6_bf16(bf16x8 ah, bf16x8 am, bf16x8 al, bf16x8 bh,
+                                              bf16x8 bm, bf16x8 bl, floatx4 c) {
+  c = mfma_16x16x32_bf16(al, bh, c);
+  c = mfma_16x16x32_bf16(ah, bl, c);
+  c = mfma_16x16x32_bf16(am, bm, c);
+  c = mfma_16x16x32_bf16(am, bh, c);
+  c = mfma_16x16x32_bf16(ah, bm, c);
+  return mfma_16x16x32_bf16(ah, bh, c);
+}
+
+// The attention core on the bf16 matrix cores (head_dim 32, 64 or 128).
+// Same workgroup, lane and softmax layout as attention_kernel; every fp32
+// operand is split into three bf16 parts (x = h + m + l to about 2^-27 |x|)
+// and each product takes the six part products above 2^-18 of it, 16x16x32
+// bf16 MFMAs: within about 2^-25 of the fp32 product, against 16x16x4 fp32
+// MFMAs at a sixteenth of the rate.  K is staged as three bf16 planes
+// [key][dim]; V transposed, [dim][key], so that O^T = V^T . P^T takes P^T
+// straight from the score registers: a lane of group g holds keys
+// 16 ks + 4 g + i of subtiles ks and ks + 1, and reads the same eight keys of
+// V^T as two 8-byte runs.  The next key block's K and V are loaded into
+// registers while the current one is multiplied.
+template <int DH, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void attention_bf16_kernel(const float* __restrict__ q,
+                                                             const float* __restrict__ k,
+                                                             const float* __restrict__ v,
+                                                             AttnShape sh,
+                                                             float* __restrict__ out) {
+  constexpr int KP = DH + 8;             // K plane pitch (bf16): conflict-free 16-byte reads
+  constexpr int VP = kAttnKB + 4;        // V^T plane pitch (bf16): conflict-free 8-byte reads
+  constexpr int K_PLANE = kAttnKB * KP;  // elements per plane
+  constexpr int V_PLANE = DH * VP;
+  constexpr int ST = DH / 32;            // 32-dim steps of S^T
+  constexpr int DT = DH / 16;            // 16-dim output tiles
+  constexpr int NT = 64 * WAVES, QB = 16 * WAVES;         // threads, queries per workgroup
+  constexpr int KITEMS = kAttnKB * DH / 4 / NT;           // K float4s per thread
+  constexpr int VITEMS = (4 * DH + NT - 1) / NT;          // 4 keys x 4 dims V items per thread
+  constexpr int OPITCH = DH + 4;                          // output staging pitch (floats)
+  static_assert(DH % 32 == 0 && KITEMS >= 1, "head_dim 32, 64 or 128");
+  static_assert(WAVES * 16 * OPITCH * 4 <= 3 * (K_PLANE + V_PLANE) * 2,
+                "output staging fits the planes");
+  extern __shared__ __align__(16) uint16_t attn_lds[];
+  uint16_t* kl = attn_lds;                 // 3 planes [key][dim]
+  uint16_t* vl = attn_lds + 3 * K_PLANE;   // 3 planes [dim][key]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int64_t b = blockIdx.z;
+  const int h = blockIdx.y;
+  const int kvh = h / (sh.heads / sh.kv_heads);
+  const int64_t qblk0 = int64_t(blockIdx.x) * QB;
+  const int64_t qi = qblk0 + wave * 16 + col;  // this lane's query
+  const int64_t S = sh.seq_q, SK = sh.seq_k;
+  const int64_t qpos = sh.q_pos0 + qi;
+  const float* qb = q + (b * sh.q_bstride) * sh.ldq + int64_t(h) * DH;
+  const float* kb = k + (b * sh.kv_bstride) * sh.ldk + int64_t(kvh) * DH;
+  const float* vb = v + (b * sh.kv_bstride) * sh.ldv + int64_t(kvh) * DH;
+
+  // Q^T operand of step st: dims 32 st + 8 grp + [0, 8) of query qi
+  bf16x8 qh[ST], qm[ST], ql[ST];
+#pragma unroll
+  for (int st = 0; st < ST; ++st) {
+    float x[8];
+    const float* src = qb + (qi < S ? qi : 0) * sh.ldq + st * 32 + 8 * grp;
+    const float4 a = *reinterpret_cast<const float4*>(src);
+    const float4 c = *reinterpret_cast<const float4*>(src + 4);
+    const bool live = qi < S;
+    x[0] = live ? a.x : 0.f; x[1] = live ? a.y : 0.f; x[2] = live ? a.z : 0.f; x[3] = live ? a.w : 0.f;
+    x[4] = live ? c.x : 0.f; x[5] = live ? c.y : 0.f; x[6] = live ? c.z : 0.f; x[7] = live ? c.w : 0.f;
+    split3_bf16x8(x, qh[st], qm[st], ql[st]);
+  }
+
+  floatx4 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;
+  float l_part = 0.0f;
+
+  const int64_t q_last = (qblk0 + QB - 1 < S - 1) ? qblk0 + QB - 1 : S - 1;
+  const int64_t rel_last = sh.q_pos0 + q_last - sh.k_pos0;
+  const int64_t rel_first = sh.q_pos0 + qblk0 - sh.k_pos0;
+  int64_t key_end = SK;
+  if (sh.causal && rel_last + 1 < key_end) key_end = rel_last + 1;
+  if (sh.window >= 0 && rel_last + sh.window + 1 < key_end) key_end = rel_last + sh.window + 1;
+  int64_t key_begin = 0;
+  if (sh.window >= 0 && rel_first - sh.window > 0) key_begin = rel_first - sh.window;
+  if (key_end < 0) key_end = 0;
+  const int64_t kb_begin = key_begin / kAttnKB;
+  const int64_t kb_end = (key_end + kAttnKB - 1) / kAttnKB;
+
+  // a key block's K (float4 of one key) and V (4 keys x 4 dims) in
+  // registers; keys past the sequence read key 0 and are zeroed when staged
+  float4 kreg[KITEMS], vreg[VITEMS][4];
+  auto load_block = [&](int64_t key0) {
+#pragma unroll
+    for (int it = 0; it < KITEMS; ++it) {
+      const int idx = tid + it * NT, r = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+      const int64_t key = key0 + r;
+      kreg[it] = *reinterpret_cast<const float4*>(kb + (key < SK ? key : 0) * sh.ldk + c4);
+    }
+#pragma unroll
+    for (int it = 0; it < VITEMS; ++it) {
+      const int idx = tid + it * NT;
+      const int item = idx < 4 * DH ? idx : 0;
+      const int kg = item / (DH / 4), d4 = (item % (DH / 4)) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t key = key0 + 4 * kg + j;
+        vreg[it][j] = *reinterpret_cast<const float4*>(vb + (key < SK ? key : 0) * sh.ldv + d4);
+      }
+    }
+  };
+  auto store_block = [&](int64_t key0) {
+#pragma unroll
+    for (int it = 0; it < KITEMS; ++it) {
+      const int idx = tid + it * NT, r = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+      const bool live = key0 + r < SK;
+      const float4 t = live ? kreg[it] : make_float4(0.f, 0.f, 0.f, 0.f);
+      uint32_t h0, m0, l0, h1, m1, l1;
+      split3_bf16x2(t.x, t.y, h0, m0, l0);
+      split3_bf16x2(t.z, t.w, h1, m1, l1);
+      uint16_t* dst = kl + r * KP + c4;
+      *reinterpret_cast<uint2*>(dst) = make_uint2(h0, h1);
+      *reinterpret_cast<uint2*>(dst + K_PLANE) = make_uint2(m0, m1);
+      *reinterpret_cast<uint2*>(dst + 2 * K_PLANE) = make_uint2(l0, l1);
+    }
+#pragma unroll
+    for (int it = 0; it < VITEMS; ++it) {
+      const int idx = tid + it * NT;
+      if (idx < 4 * DH) {
+        const int kg = idx / (DH / 4), d4 = (idx % (DH / 4)) * 4;
+        float4 t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          t[j] = key0 + 4 * kg + j < SK ? vreg[it][j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float x[4][4] = {{t[0].x, t[1].x, t[2].x, t[3].x}, {t[0].y, t[1].y, t[2].y, t[3].y},
+                               {t[0].z, t[1].z, t[2].z, t[3].z}, {t[0].w, t[1].w, t[2].w, t[3].w}};
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) {
+          uint32_t h0, m0, l0, h1, m1, l1;
+          split3_bf16x2(x[dd][0], x[dd][1], h0, m0, l0);
+          split3_bf16x2(x[dd][2], x[dd][3], h1, m1, l1);
+          uint16_t* dst = vl + (d4 + dd) * VP + 4 * kg;
+          *reinterpret_cast<uint2*>(dst) = make_uint2(h0, h1);
+          *reinterpret_cast<uint2*>(dst + V_PLANE) = make_uint2(m0, m1);
+          *reinterpret_cast<uint2*>(dst + 2 * V_PLANE) = make_uint2(l0, l1);
+        }
+      }
+    }
+  };
+
+  if (kb_begin < kb_end) load_block(kb_begin * kAttnKB);
+  for (int64_t blk = kb_begin; blk < kb_end; ++blk) {
+    const int64_t key0 = blk * kAttnKB;
+    __syncthreads();  // the previous block's planes are no longer read
+    store_block(key0);
+    __syncthreads();
+    if (blk + 1 < kb_end) load_block(key0 + kAttnKB);  // in flight during the products
+
+    // S^T: 4 subtiles of 16 keys; lane holds keys 16 ks + 4 grp + i of query qi
+    floatx4 s[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      s[ks] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < ST; ++st) {
+        const uint16_t* kr = kl + (ks * 16 + col) * KP + st * 32 + 8 * grp;
+        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(kr);
+        const bf16x8 am = *reinterpret_cast<const bf16x8*>(kr + K_PLANE);
+        const bf16x8 al = *reinterpret_cast<const bf16x8*>(kr + 2 * K_PLANE);
+        s[ks] = mfma6_bf16(ah, am, al, qh[st], qm[st], ql[st], s[ks]);
+      }
+    }
+    // scale (into log2 units), mask, block max.  Key 16 ks + 4 grp + i of
+    // the block is allowed for this lane's query iff it lies in [jlo, jhi)
+    // (the sequence end, causality and the window as bounds on the key
+    // index); a wave whose queries all see the whole block skips the masks.
+    const int64_t rel = qpos - sh.k_pos0 - key0;  // the query's position as a key index
+    int64_t jhi = SK - key0, jlo = 0;
+    if (sh.causal && rel + 1 < jhi) jhi = rel + 1;
+    if (sh.window >= 0) {
+      if (rel + sh.window + 1 < jhi) jhi = rel + sh.window + 1;
+      if (rel - sh.window > jlo) jlo = rel - sh.window;
+    }
+    const int lo32 = int(jlo < kAttnKB ? jlo : kAttnKB) - 4 * grp;
+    const int hi32 = int(jhi > 0 ? (jhi < kAttnKB ? jhi : kAttnKB) : 0) - 4 * grp;
+    const float sc = sh.scale * 1.44269504088896341f;  // log2(e)
+    float mx = -INFINITY;
+    if (__all(lo32 <= -4 * grp && hi32 >= kAttnKB - 4 * grp)) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s[ks][i] *= sc;
+          mx = fmaxf(mx, s[ks][i]);
+        }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int c = ks * 16 + i;
+          const float val = (c >= lo32 && c < hi32) ? s[ks][i] * sc : -INFINITY;
+          s[ks][i] = val;
+          mx = fmaxf(mx, val);
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    float psum = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = __builtin_amdgcn_exp2f(s[ks][i] - m_use);
+        s[ks][i] = p;
+        psum += p;
+      }
+    l_part = l_part * alpha + psum;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] *= alpha;
+
+    // O^T += V^T . P^T over two 32-key steps
+#pragma unroll
+    for (int kp = 0; kp < 2; ++kp) {
+      const float pv[8] = {s[2 * kp][0], s[2 * kp][1], s[2 * kp][2], s[2 * kp][3],
+                           s[2 * kp + 1][0], s[2 * kp + 1][1], s[2 * kp + 1][2], s[2 * kp + 1][3]};
+      bf16x8 ph, pm, pl;
+      split3_bf16x8(pv, ph, pm, pl);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const uint16_t* vr = vl + (16 * t + col) * VP + 32 * kp + 4 * grp;
+        bf16x8 a[3];
+#pragma unroll
+        for (int pl3 = 0; pl3 < 3; ++pl3) {
+          const uint2 lo = *reinterpret_cast<const uint2*>(vr + pl3 * V_PLANE);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vr + pl3 * V_PLANE + 16);
+          a[pl3] = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        }
+        o[t] = mfma6_bf16(a[0], a[1], a[2], ph, pm, pl, o[t]);
+      }
+    }
+  }
+
+  // total sum over the four lanes of this query; normalise; write through
+  // LDS (the K planes, no longer read) so each query row leaves as float4s
+  float l_tot = l_part + __shfl_xor(l_part, 16, 64);
+  l_tot = l_tot + __shfl_xor(l_tot, 32, 64);
+  __syncthreads();
+  float* my = reinterpret_cast<float*>(attn_lds) + wave * 16 * OPITCH;
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) my[col * OPITCH + t * 16 + 4 * grp + r] = o[t][r] / l_tot;
+  __syncthreads();
+  for (int idx = lane; idx < 16 * (DH / 4); idx += 64) {
+    const int r = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+    const int64_t qq = qblk0 + wave * 16 + r;
+    if (qq < S)
+      *reinterpret_cast<float4*>(out + (b * sh.q_bstride + qq) * sh.ldo + int64_t(h) * DH + c4) =
+          *reinterpret_cast<const float4*>(&my[r * OPITCH + c4]);
+  }
+}
+
+// 8 waves (128 queries) per workgroup: each staged K / V block serves twice
+// the queries of the fp32 kernel's 64
+constexpr int kAttnWaves = 8;
+
+template <int DH>
+void launch_attention_bf16(const float* q, const float* k, const float* v, const AttnShape& sh,
+                           float* out) {
+  constexpr size_t lds = size_t(3) * (kAttnKB * (DH + 8) + DH * (kAttnKB + 4)) * sizeof(uint16_t);
+  auto kernel = attention_bf16_kernel<DH, kAttnWaves>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    ENQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    attr_set = true;
+  }
+  const dim3 grid(unsigned(ceil_div(sh.seq_q, int64_t(16 * kAttnWaves))), unsigned(sh.heads),
+                  unsigned(sh.batch));
+  kernel<<<grid, 64 * kAttnWaves, lds, stream()>>>(q, k, v, sh, out);
+}
+
 void attention(const float* q, const float* k, const float* v, const AttnShape& sh, int head_dim,
                float* out) {
   const dim3 grid(unsigned(ceil_div(sh.seq_q, kAttnQ)), unsigned(sh.heads), unsigned(sh.batch));
@@ -399,13 +724,13 @@ void attention(const float* q, const float* k, const float* v, const AttnShape& 
       attention_kernel<16><<<grid, 256, 0, stream()>>>(q, k, v, sh, out);
       break;
     case 32:
-      attention_kernel<32><<<grid, 256, 0, stream()>>>(q, k, v, sh, out);
+      launch_attention_bf16<32>(q, k, v, sh, out);
       break;
     case 64:
-      attention_kernel<64><<<grid, 256, 0, stream()>>>(q, k, v, sh, out);
+      launch_attention_bf16<64>(q, k, v, sh, out);
       break;
     case 128:
-      attention_kernel<128><<<grid, 256, 0, stream()>>>(q, k, v, sh, out);
+      launch_attention_bf16<128>(q, k, v, sh, out);
       break;
     default:
       fail(ENQ_ERR_UNSUPPORTED, "attention head_dim %d is not one of 16, 32, 64, 128", head_dim);

@@ -4,8 +4,9 @@
   float64 oracle (``nn/forward.py:207-254``).
 * Residual add: bit-identical to NumPy's float32 sum.
 * Attention core: max |ctx - ctx_ref| <= 2e-5 * max |ctx_ref| per row
-  against float64 attention on the same Q, K, V (fp32 MFMA products,
-  fp32 sums and exponentials).
+  against float64 attention on the same Q, K, V (head_dim 16: fp32 MFMA
+  products; 32-128: each fp32 operand split into three bf16 parts, six
+  bf16 MFMA part products per product; fp32 sums and exponentials).
 * Multi-head attention layer and transformer block through ``Forward``:
   the Dense bound, max |y - y_ref| <= 1e-4 * max |y_ref| per row, against the
   float64 oracle on the fake-quantized weights; host dtypes follow NumPy's
@@ -77,6 +78,7 @@ ATTN_CASES = [
     (2, 77, 4, 1, 16, True, None),
     (1, 200, 2, 2, 128, False, 5),
     (1, 70, 2, 2, 64, True, 0),
+    (2, 300, 4, 2, 64, True, None),
     (3, 1, 2, 1, 64, False, None),
     (8, 512, 16, 16, 64, False, None),
 ]
