@@ -448,10 +448,14 @@ __device__ __forceinline__ floatx4 mfma6_bf16(bf16x8 ah, bf16x8 am, bf16x8 al, b
 // [key][dim]; V transposed, [dim][key], so that O^T = V^T . P^T takes P^T
 // straight from the score registers: a lane of group g holds keys
 // 16 ks + 4 g + i of subtiles ks and ks + 1, and reads the same eight keys of
-// V^T as two 8-byte runs.  The next key block's K and V are loaded into
-// registers while the current one is multiplied.
+// V^T as two 8-byte runs.  Up to head_dim 64 the registers are held to 128
+// so that two 8-wave workgroups share a CU (B8 S512 H16 D64: 75.0 -> 69.8 us;
+// holding the next key block's K and V in registers during the products
+// does not fit in that budget).
 template <int DH, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void attention_bf16_kernel(const float* __restrict__ q,
+__global__ __launch_bounds__(64 * WAVES)
+__attribute__((amdgpu_waves_per_eu(DH <= 64 ? WAVES / 2 : 1, DH <= 64 ? WAVES / 2 : 2)))
+void attention_bf16_kernel(const float* __restrict__ q,
                                                              const float* __restrict__ k,
                                                              const float* __restrict__ v,
                                                              AttnShape sh,
@@ -579,13 +583,12 @@ __global__ __launch_bounds__(64 * WAVES) void attention_bf16_kernel(const float*
     }
   };
 
-  if (kb_begin < kb_end) load_block(kb_begin * kAttnKB);
   for (int64_t blk = kb_begin; blk < kb_end; ++blk) {
     const int64_t key0 = blk * kAttnKB;
+    load_block(key0);
     __syncthreads();  // the previous block's planes are no longer read
     store_block(key0);
     __syncthreads();
-    if (blk + 1 < kb_end) load_block(key0 + kAttnKB);  // in flight during the products
 
     // S^T: 4 subtiles of 16 keys; lane holds keys 16 ks + 4 grp + i of query qi
     floatx4 s[4];
