@@ -354,7 +354,10 @@ int enq_add(const float* a, const float* b, int64_t n, float* y);
  * occupies columns [h*D, (h+1)*D); a fused QKV projection output is passed
  * as three pointers into one buffer with the same row stride.  head_dim is
  * 16, 32, 64 or 128 (other values: ENQ_ERR_UNSUPPORTED); rows 16-byte
- * aligned. */
+ * aligned.  Products are fp32-accurate: at head_dim 32-128 each is six bf16
+ * matrix-core products of the operands' three-part bf16 splits (within about
+ * 2^-25 of the fp32 product), at 16 an fp32 matrix-core product; sums and
+ * exponentials are fp32. */
 int enq_attention(const float* q, int64_t ldq, const float* k, int64_t ldk,
                   const float* v, int64_t ldv, int64_t batch, int64_t seq,
                   int heads, int kv_heads, int head_dim, int causal,
