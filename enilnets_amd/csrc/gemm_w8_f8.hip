@@ -579,10 +579,14 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
               yo.lo[row * yo.ld + col] =
                   uint8_t(__builtin_amdgcn_cvt_pk_fp8_f32(a - static_cast<float>(h), 0.0f, 0, false));
             } else if (ksplit > 1) {
-              y[int64_t(part) * m * n + row * n + col] = v;
+              __builtin_nontemporal_store(v, &y[int64_t(part) * m * n + row * n + col]);
             } else {
-              if (z) z[row * n + col] = v;
-              y[row * n + col] = act(v);
+              // non-temporal: every CU writes its tile at the same moment at
+              // the end of a round; streamed past the L2 the stores cost 1-4%
+              // less (4096 x 1024 x 4096: 85.8 -> 82.0 us, the transformer
+              // block 441 -> 432 us)
+              if (z) __builtin_nontemporal_store(v, &z[row * n + col]);
+              __builtin_nontemporal_store(act(v), &y[row * n + col]);
             }
           }
         }
