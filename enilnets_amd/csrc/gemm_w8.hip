@@ -981,7 +981,7 @@ void w8_ring_kernel(
           if (row < m_end) {
             float v = acc[i][j][e] * s;
             if (bias) v = v + b;
-            if (z) z[row * n + col] = v;
+            if (z) __builtin_nontemporal_store(v, &z[row * n + col]);
             if constexpr (YP) {
               // the output as the next GEMM's bf16 planes (split_planes_kernel's split)
               const float h = act(v);
@@ -990,7 +990,7 @@ void w8_ring_kernel(
               if constexpr (PLANES == 2)
                 yp[yp_plane_stride + row * yp_ld + col] = bf16_bits_rne(h - bf16_to_float(hi));
             } else {
-              y[row * n + col] = act(v);
+              __builtin_nontemporal_store(act(v), &y[row * n + col]);
             }
           }
         }

@@ -400,11 +400,11 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
           const int64_t row = row0 + 8 * (e / 4) + (e % 4);
           if (row < m) {
             const int32_t a = acc[i][j][e] + add[j];
-            if (acc_out) acc_out[row * n + col] = a;
+            if (acc_out) __builtin_nontemporal_store(a, &acc_out[row * n + col]);
             float v = float(a) * xs[e];
             v = v * sw[j];
             if (bias) v = v + bj[j];
-            y[row * n + col] = act(v);
+            __builtin_nontemporal_store(act(v), &y[row * n + col]);
           }
         }
       });
