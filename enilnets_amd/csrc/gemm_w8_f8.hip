@@ -559,12 +559,34 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
         if constexpr (YF8) eo[e] = yo.exps[row < m ? row : m - 1];
       }
       const int64_t row0 = m0 + wm * TM + i * 32 + 4 * lhalf;
+      // the wave's 32 rows all inside the tile's rows (every block of a full
+      // tile): no per-element row test, and the rows' offsets (8 q + r) * n
+      // are wave-uniform
+      const bool rows_in = m0 + wm * TM + i * 32 + 32 <= m_end;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int64_t col = n0 + wn * TN + j * 32 + lrow;
         if (col >= n) continue;
         const float s = scale[col];
         const float b = bias && part == 0 ? bias[col] : 0.f;
+        if constexpr (!YF8) {
+          if (rows_in) {
+            const int64_t at = (ksplit > 1 ? int64_t(part) * m * n : 0) + row0 * n + col;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int64_t off = at + int64_t(8 * (e / 4) + (e % 4)) * n;
+              float v = ldexpf(acc[i][j][e], ex[e]) * s;
+              if (bias && part == 0) v = v + b;
+              if (ksplit > 1) {
+                __builtin_nontemporal_store(v, &y[off]);
+              } else {
+                if (z) __builtin_nontemporal_store(v, &z[off]);
+                __builtin_nontemporal_store(act(v), &y[off]);
+              }
+            }
+            continue;
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int64_t row = row0 + 8 * (e / 4) + (e % 4);
