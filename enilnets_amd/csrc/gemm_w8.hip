@@ -974,7 +974,24 @@ void w8_ring_kernel(
       const float s = col_scale[j];
       const float b = col_bias[j];
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i) {
+        if constexpr (!YP && C::BM <= 128) {
+          // the wave's 32 rows all inside the tile's rows: no per-element
+          // row test, wave-uniform row offsets (8 q + r) * n (the 256 x 256
+          // tiles spill 37 VGPRs with this path)
+          if (m0 + wm * TM + i * 32 + 32 <= m_end) {
+            const int64_t at = (m0 + wm * TM + i * 32 + 4 * lhalf) * n + col;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int64_t off = at + int64_t(8 * (e / 4) + (e % 4)) * n;
+              float v = acc[i][j][e] * s;
+              if (bias) v = v + b;
+              if (z) __builtin_nontemporal_store(v, &z[off]);
+              __builtin_nontemporal_store(act(v), &y[off]);
+            }
+            continue;
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int64_t row = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * lhalf + (e % 4);
@@ -994,6 +1011,7 @@ void w8_ring_kernel(
             }
           }
         }
+      }
     }
   });
 }

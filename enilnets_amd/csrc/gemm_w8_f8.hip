@@ -569,7 +569,23 @@ void w8_f8_ring_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restric
         if (col >= n) continue;
         const float s = scale[col];
         const float b = bias && part == 0 ? bias[col] : 0.f;
-        if constexpr (!YF8) {
+        if constexpr (YF8) {
+          if (rows_in) {
+            const int64_t at = row0 * yo.ld + col;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int64_t off = at + int64_t(8 * (e / 4) + (e % 4)) * yo.ld;
+              float v = ldexpf(acc[i][j][e], ex[e]) * s;
+              if (bias && part == 0) v = v + b;
+              const float a = ldexpf(act(v), eo[e]);
+              const _Float16 h = static_cast<_Float16>(a);
+              yo.hi[off] = __builtin_bit_cast(uint16_t, h);
+              yo.lo[off] =
+                  uint8_t(__builtin_amdgcn_cvt_pk_fp8_f32(a - static_cast<float>(h), 0.0f, 0, false));
+            }
+            continue;
+          }
+        } else {
           if (rows_in) {
             const int64_t at = (ksplit > 1 ? int64_t(part) * m * n : 0) + row0 * n + col;
 #pragma unroll

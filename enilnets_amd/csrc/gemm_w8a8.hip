@@ -395,6 +395,22 @@ __global__ __launch_bounds__(R::NT, 1) void w8a8_ring_kernel(
         constexpr int j = decltype(jc)::value;
         const int64_t col = n0 + wn * TN + j * 32 + lrow;
         if (col >= n) return;
+        if (m0 + wm * TM + i * 32 + 32 <= m) {
+          // the wave's 32 rows all inside the output: no per-element row
+          // test, wave-uniform row offsets (8 q + r) * n
+          const int64_t at = row0 * n + col;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int64_t off = at + int64_t(8 * (e / 4) + (e % 4)) * n;
+            const int32_t a = acc[i][j][e] + add[j];
+            if (acc_out) __builtin_nontemporal_store(a, &acc_out[off]);
+            float v = float(a) * xs[e];
+            v = v * sw[j];
+            if (bias) v = v + bj[j];
+            __builtin_nontemporal_store(act(v), &y[off]);
+          }
+          return;
+        }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int64_t row = row0 + 8 * (e / 4) + (e % 4);
