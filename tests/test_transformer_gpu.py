@@ -3,7 +3,8 @@
 * LayerNorm: max |y - y_ref| <= 2e-6 * max |y_ref| per row against the
   float64 oracle (``nn/forward.py:207-254``).
 * Residual add: bit-identical to NumPy's float32 sum.
-* Attention core: max |ctx - ctx_ref| <= 2e-5 * max |ctx_ref| per row
+* Attention core, and the KV-cache step's attention (queries at positions
+  after the cached keys, enq_attention_kv): max |ctx - ctx_ref| <= 2e-5 * max |ctx_ref| per row
   against float64 attention on the same Q, K, V (head_dim 16: fp32 MFMA
   products; 32-128: each fp32 operand split into three bf16 parts, six
   bf16 MFMA part products per product; fp32 sums and exponentials).
@@ -98,6 +99,51 @@ def test_attention_core(gpu, B, S, H, Hkv, Dh, causal, window):
     _lib.call("enq_attention", d.ptr, ld, T._at(d, 4 * nq), ld, T._at(d, 4 * (nq + nkv)), ld,
               B, S, H, Hkv, Dh, int(causal), -1 if window is None else window, out.ptr, nq)
     want = attention_ref(q, k, v, H, Hkv, Dh, causal, window)
+    err = row_rel_err(out.numpy(), want)
+    assert np.all(err <= 2e-5), f"max row error {err.max():.3e}"
+
+
+KV_CASES = [
+    # B, seq_q, seq_k, H, Hkv, Dh, causal, window: the queries are the last seq_q positions
+    (2, 1, 300, 4, 2, 64, True, None),
+    (2, 3, 200, 4, 4, 128, True, 50),
+    (1, 5, 129, 2, 1, 32, False, None),
+    (3, 70, 140, 2, 2, 64, True, None),
+    (2, 1, 90, 2, 2, 16, True, 10),
+]
+
+
+@pytest.mark.parametrize("B,SQ,SK,H,Hkv,Dh,causal,window", KV_CASES)
+def test_attention_kv_core(gpu, B, SQ, SK, H, Hkv, Dh, causal, window):
+    # a KV-cache step: seq_q new queries at positions SK - SQ .. SK - 1 over
+    # SK cached keys, against float64 attention with the same position masks
+    print(f"[case] attention_kv B={B} SQ={SQ} SK={SK} H={H} Hkv={Hkv} Dh={Dh} causal={causal} "
+          f"window={window}", flush=True)
+    rng = np.random.default_rng(B * 100 + SQ + SK + Dh)
+    q = rng.standard_normal((B, SQ, H * Dh)).astype(np.float32)
+    k = rng.standard_normal((B, SK, Hkv * Dh)).astype(np.float32)
+    v = rng.standard_normal((B, SK, Hkv * Dh)).astype(np.float32)
+    d_q, d_k, d_v = DeviceArray.from_numpy(q), DeviceArray.from_numpy(k), DeviceArray.from_numpy(v)
+    out = DeviceArray((B, SQ, H * Dh), np.float32)
+    q_pos0 = SK - SQ
+    _lib.call("enq_attention_kv", d_q.ptr, H * Dh, SQ, SQ, q_pos0, d_k.ptr, Hkv * Dh, d_v.ptr,
+              Hkv * Dh, SK, SK, 0, B, H, Hkv, Dh, int(causal), -1 if window is None else window,
+              out.ptr, H * Dh)
+    qh = q.reshape(B, SQ, H, Dh).transpose(0, 2, 1, 3).astype(np.float64)
+    kh = np.repeat(k.reshape(B, SK, Hkv, Dh).transpose(0, 2, 1, 3).astype(np.float64), H // Hkv, 1)
+    vh = np.repeat(v.reshape(B, SK, Hkv, Dh).transpose(0, 2, 1, 3).astype(np.float64), H // Hkv, 1)
+    s = qh @ kh.transpose(0, 1, 3, 2) / np.sqrt(Dh)
+    qpos = q_pos0 + np.arange(SQ)[:, None]
+    kpos = np.arange(SK)[None, :]
+    allowed = np.ones((SQ, SK), bool)
+    if causal:
+        allowed &= kpos <= qpos
+    if window is not None:
+        allowed &= np.abs(qpos - kpos) <= window
+    s = np.where(allowed, s, -np.inf)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    want = (p @ vh).transpose(0, 2, 1, 3).reshape(B, SQ, H * Dh)
     err = row_rel_err(out.numpy(), want)
     assert np.all(err <= 2e-5), f"max row error {err.max():.3e}"
 
