@@ -213,7 +213,9 @@ __device__ __forceinline__ float fmin_t<float>(float a, float b) { return __buil
 template <>
 __device__ __forceinline__ double fmin_t<double>(double a, double b) { return __builtin_fmin(a, b); }
 
-template <class T, int TPR, int CHUNKS, int V, bool SYM, int OUT>
+// GIVEN: one scale and zero point for every row, read from scale_out[0] and
+// zp_out[0] (the codes pass of a per-tensor quantize), no row statistics.
+template <class T, int TPR, int CHUNKS, int V, bool SYM, int OUT, bool GIVEN = false>
 __global__ __launch_bounds__(TPR < kBlock ? kBlock : TPR) void rows_quant_kernel(
     const T* __restrict__ w, int64_t rows, int64_t cols, QParams p,
     T* __restrict__ out_fake, int8_t* __restrict__ out_codes,
@@ -253,55 +255,60 @@ __global__ __launch_bounds__(TPR < kBlock ? kBlock : TPR) void rows_quant_kernel
   // not change max |x|; for min / max they are excluded below.
   T a = SYM ? T(0) : pos_inf<T>(), b = -pos_inf<T>();
   int nan = 0;
+  if constexpr (!GIVEN) {
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int64_t idx = (int64_t(c) * TPR + t) * V;
-    const bool live = SYM || (active && idx < cols);
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int64_t idx = (int64_t(c) * TPR + t) * V;
+      const bool live = SYM || (active && idx < cols);
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      const T x = vals[c][e];
-      nan |= (x != x);
-      if (SYM) {
-        a = fmax_t(a, x < T(0) ? -x : x);
-      } else if (live) {
-        a = fmin_t(a, x);
-        b = fmax_t(b, x);
+      for (int e = 0; e < V; ++e) {
+        const T x = vals[c][e];
+        nan |= (x != x);
+        if (SYM) {
+          a = fmax_t(a, x < T(0) ? -x : x);
+        } else if (live) {
+          a = fmin_t(a, x);
+          b = fmax_t(b, x);
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      a = SYM ? fmax_t(a, __shfl_xor(a, m, 64)) : fmin_t(a, __shfl_xor(a, m, 64));
+      if (!SYM) b = fmax_t(b, __shfl_xor(b, m, 64));
+      nan |= __shfl_xor(nan, m, 64);
+    }
+    if constexpr (kWavesPerRow > 1) {
+      const int wave = threadIdx.x / 64;
+      if ((threadIdx.x & 63) == 0) {
+        s_a[wave] = a;
+        if (!SYM) s_b[wave] = b;
+        s_nan[wave] = nan;
+      }
+      __syncthreads();
+      const int first = (threadIdx.x / TPR) * kWavesPerRow;
+      a = s_a[first];
+      if (!SYM) b = s_b[first];
+      nan = s_nan[first];
+#pragma unroll
+      for (int i = 1; i < kWavesPerRow; ++i) {
+        a = SYM ? fmax_t(a, s_a[first + i]) : fmin_t(a, s_a[first + i]);
+        if (!SYM) b = fmax_t(b, s_b[first + i]);
+        nan |= s_nan[first + i];
       }
     }
   }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    a = SYM ? fmax_t(a, __shfl_xor(a, m, 64)) : fmin_t(a, __shfl_xor(a, m, 64));
-    if (!SYM) b = fmax_t(b, __shfl_xor(b, m, 64));
-    nan |= __shfl_xor(nan, m, 64);
-  }
-  if constexpr (kWavesPerRow > 1) {
-    const int wave = threadIdx.x / 64;
-    if ((threadIdx.x & 63) == 0) {
-      s_a[wave] = a;
-      if (!SYM) s_b[wave] = b;
-      s_nan[wave] = nan;
-    }
-    __syncthreads();
-    const int first = (threadIdx.x / TPR) * kWavesPerRow;
-    a = s_a[first];
-    if (!SYM) b = s_b[first];
-    nan = s_nan[first];
-#pragma unroll
-    for (int i = 1; i < kWavesPerRow; ++i) {
-      a = SYM ? fmax_t(a, s_a[first + i]) : fmin_t(a, s_a[first + i]);
-      if (!SYM) b = fmax_t(b, s_b[first + i]);
-      nan |= s_nan[first + i];
-    }
-  }
   T scale, zp;
-  if (SYM) {
+  if constexpr (GIVEN) {
+    scale = scale_out[0];
+    zp = zp_out[0];
+  } else if (SYM) {
     // compute_scale with low = -a, high = a gives max(|low|, |high|) = a
     scale_from_range(nan ? nan_value<T>() : -a, nan ? nan_value<T>() : a, p, scale, zp);
   } else {
     scale_from_range(nan ? nan_value<T>() : a, nan ? nan_value<T>() : b, p, scale, zp);
   }
-  if (active && t == 0) {
+  if (!GIVEN && active && t == 0) {
     scale_out[row] = scale;
     zp_out[row] = zp;
   }
@@ -1259,10 +1266,11 @@ void quantize_tensor_impl(const T* w, int64_t outer, int64_t channels, int64_t i
   if constexpr (std::is_same_v<T, float>) {
     if (channels == 1 && aligned(w, 16) && (fake == nullptr || aligned(fake, 16)) &&
         (codes == nullptr || aligned(codes, 16))) {
-      // per-tensor: the statistics pass, then one launch that finishes the
-      // statistics in every workgroup and quantizes.  8192 x 8192 to int8
-      // codes: 120-128 us as statistics, finish_range_kernel and the
-      // elementwise pass
+      // per-tensor: the statistics pass, then either the row kernel with the
+      // one finished scale (whole rows of 8192 values, no error sum) or one
+      // launch that finishes the statistics in every workgroup and
+      // quantizes.  8192 x 8192 to int8 codes took 120-128 us as statistics,
+      // finish_range_kernel and the elementwise pass
       const int sgrid = grid_for(ceil_div(n, 16));
       const int qgrid = int(std::min<int64_t>(ceil_div(n, int64_t(kBlock) * 16),
                                               int64_t(device_cu_count()) * 8));
@@ -1272,6 +1280,26 @@ void quantize_tensor_impl(const T* w, int64_t outer, int64_t channels, int64_t i
       double* err_part = abs_err ? reinterpret_cast<double*>(ws + part_bytes) : nullptr;
       minmax_flat_kernel<float, 4><<<sgrid, kBlock, 0, stream()>>>(w, n, part);
       check_launch("minmax_flat_kernel");
+      if (!abs_err && n % 8192 == 0 && n / 8192 <= 0x7fffffff) {
+        // the range in one workgroup, then the row kernel over rows of 8192
+        // values with that one scale: 8192 x 8192 to codes 109.4 -> 104.9 us
+        // against the pass below, whose every workgroup merges the partials
+        finish_range_kernel<float><<<1, kBlock, 0, stream()>>>(part, sgrid, 0, 1, 1, p, 1, nullptr,
+                                                               nullptr, scale, zp);
+        check_launch("finish_range_kernel");
+        const unsigned rows = unsigned(n / 8192);
+        if (fake && codes)
+          rows_quant_kernel<float, 256, 8, 4, true, kOutFake | kOutCodes, true>
+              <<<rows, 256, 0, stream()>>>(w, rows, 8192, p, fake, codes, scale, zp, nullptr);
+        else if (codes)
+          rows_quant_kernel<float, 256, 8, 4, true, kOutCodes, true>
+              <<<rows, 256, 0, stream()>>>(w, rows, 8192, p, nullptr, codes, scale, zp, nullptr);
+        else
+          rows_quant_kernel<float, 256, 8, 4, true, kOutFake, true>
+              <<<rows, 256, 0, stream()>>>(w, rows, 8192, p, fake, nullptr, scale, zp, nullptr);
+        check_launch("rows_quant_kernel");
+        return;
+      }
       auto launch = [&](auto fake_c, auto codes_c, auto err_c) {
         quantize_flat_kernel<decltype(fake_c)::value, decltype(codes_c)::value,
                              decltype(err_c)::value><<<qgrid, kBlock, 0, stream()>>>(

@@ -339,3 +339,37 @@ def test_codes_at_unaligned_offsets(gpu, offset):
         got = buf.numpy()
         assert np.array_equal(got[offset:offset + n], want_codes.reshape(-1)), entry
         assert not got[:offset].any() and not got[offset + n:].any(), entry
+
+
+# per-tensor float32 tensors of whole 8192-value rows: the range reduction,
+# then one row kernel with the shared scale; every output combination
+PER_TENSOR_ROWS = [((2, 8192), 8, "symmetric", False), ((16, 8192), 4, "asymmetric", False),
+                   ((96, 1024), 7, "asymmetric", True), ((8192, 8192), 8, "symmetric", False)]
+
+
+@pytest.mark.parametrize("shape,bits,scheme,special", PER_TENSOR_ROWS)
+def test_quantize_per_tensor_whole_rows(gpu, shape, bits, scheme, special):
+    from enilnets_amd import _lib
+    print(f"[case] per-tensor rows {shape} {bits} {scheme} special={special}", flush=True)
+    rng = np.random.default_rng(shape[0] * 31 + bits)
+    w = (rng.standard_normal(shape) * 0.05).astype(np.float32)
+    if special:
+        w.reshape(-1)[[5, 700, 9000]] = [np.inf, -0.0, 1e-42]
+    want_fake, want_scale, want_zp = oracle.quantize_tensor(w, bits, scheme, per_channel=False)
+    q = oracle.quantize(w, want_scale, want_zp, bits, scheme)
+    want_codes = np.where(np.isnan(q), 0, q).astype(np.int8)
+    d_w = DeviceArray.from_numpy(w)
+    sch = _lib.SYMMETRIC if scheme == "symmetric" else _lib.ASYMMETRIC
+    for want_f, want_c in ((True, True), (False, True), (True, False)):
+        fake = DeviceArray(shape, np.float32) if want_f else None
+        codes = DeviceArray(shape, np.int8) if want_c else None
+        scale, zp = DeviceArray((1,), np.float32), DeviceArray((1,), np.float32)
+        _lib.call("enq_quantize_tensor", _lib.F32, d_w.ptr, 1, 1, w.size, bits, sch,
+                  fake.ptr if fake else None, codes.ptr if codes else None, scale.ptr, zp.ptr,
+                  None)
+        same_bits(scale.numpy(), np.asarray(want_scale, np.float32).reshape(-1))
+        same_bits(zp.numpy(), np.asarray(want_zp, np.float32).reshape(-1))
+        if fake:
+            same_bits(fake.numpy(), want_fake)
+        if codes:
+            assert np.array_equal(codes.numpy(), want_codes)
