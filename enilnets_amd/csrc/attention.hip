@@ -727,8 +727,159 @@ void launch_attention_bf16(const float* q, const float* k, const float* v, const
     launch_attention_bf16_waves<DH, 8>(q, k, v, sh, out);
 }
 
+// Decode steps (a few queries over a KV cache): one workgroup per query and
+// head.  For one query the allowed keys are one range [jlo, jhi) (sequence
+// end, causality, window); each wave takes a contiguous part of it.  A lane
+// holds four dims of the query; LPK = DH / 4 lanes hold one key row, so one
+// 16-byte load per lane reads KPI = 64 / LPK key rows.  Each batch issues
+// all its K and V loads before any arithmetic, then the fp32 scores (dot
+// product over the key's LPK lanes), an online softmax in log2 units and
+// the weighted V rows.  The (max, sum, output) triples then merge across
+// the wave's key slots and across the waves.  No LDS staging, no barrier
+// per key block: the K and V rows are read once, straight into registers.
+template <int DH, int WAVES, int ITB>
+__global__ __launch_bounds__(64 * WAVES) void attention_decode_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    AttnShape sh, float* __restrict__ out) {
+  constexpr int LPK = DH / 4, KPI = 64 / LPK;
+  __shared__ float s_m[WAVES], s_l[WAVES];
+  __shared__ __align__(16) float s_o[WAVES][DH];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int slot = lane / LPK, d4 = (lane % LPK) * 4;
+  const int64_t qi = blockIdx.x, b = blockIdx.z;
+  const int h = blockIdx.y;
+  const int kvh = h / (sh.heads / sh.kv_heads);
+  const int64_t SK = sh.seq_k;
+  const float* kb = k + (b * sh.kv_bstride) * sh.ldk + int64_t(kvh) * DH + d4;
+  const float* vb = v + (b * sh.kv_bstride) * sh.ldv + int64_t(kvh) * DH + d4;
+  const float4 qv =
+      *reinterpret_cast<const float4*>(q + (b * sh.q_bstride + qi) * sh.ldq + int64_t(h) * DH + d4);
+
+  const int64_t rel = sh.q_pos0 + qi - sh.k_pos0;  // the query's position as a key index
+  int64_t jhi = SK, jlo = 0;
+  if (sh.causal && rel + 1 < jhi) jhi = rel + 1;
+  if (sh.window >= 0) {
+    if (rel + sh.window + 1 < jhi) jhi = rel + sh.window + 1;
+    if (rel - sh.window > jlo) jlo = rel - sh.window;
+  }
+  const int64_t nk = jhi > jlo ? jhi - jlo : 0;
+  const int64_t chunk = (nk + WAVES * KPI - 1) / (WAVES * KPI) * KPI;
+  const int64_t wb = jlo + wave * chunk;
+  const int64_t we = wb + chunk < jhi ? wb + chunk : jhi;
+  const int64_t nit = we > wb ? (we - wb + KPI - 1) / KPI : 0;  // wave-uniform
+
+  const float sc = sh.scale * 1.44269504088896341f;  // log2(e)
+  float m_run = -INFINITY, l = 0.0f;
+  float o[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t it0 = 0; it0 < nit; it0 += ITB) {
+    float4 kr[ITB], vr[ITB];
+#pragma unroll
+    for (int it = 0; it < ITB; ++it) {
+      const int64_t j = wb + (it0 + it) * KPI + slot;
+      const int64_t jc = j < we ? j : we - 1;  // in [wb, we): we > wb here
+      kr[it] = *reinterpret_cast<const float4*>(kb + jc * sh.ldk);
+    }
+#pragma unroll
+    for (int it = 0; it < ITB; ++it) {
+      const int64_t j = wb + (it0 + it) * KPI + slot;
+      const int64_t jc = j < we ? j : we - 1;
+      vr[it] = *reinterpret_cast<const float4*>(vb + jc * sh.ldv);
+    }
+    float s[ITB];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int it = 0; it < ITB; ++it) {
+      float d = qv.x * kr[it].x;
+      d = fmaf(qv.y, kr[it].y, d);
+      d = fmaf(qv.z, kr[it].z, d);
+      d = fmaf(qv.w, kr[it].w, d);
+#pragma unroll
+      for (int m = 1; m < LPK; m <<= 1) d += __shfl_xor(d, m, 64);
+      const int64_t j = wb + (it0 + it) * KPI + slot;
+      s[it] = j < we ? d * sc : -INFINITY;
+      mx = fmaxf(mx, s[it]);
+    }
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    l *= alpha;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] *= alpha;
+#pragma unroll
+    for (int it = 0; it < ITB; ++it) {
+      const float p = __builtin_amdgcn_exp2f(s[it] - m_use);
+      l += p;
+      o[0] = fmaf(p, vr[it].x, o[0]);
+      o[1] = fmaf(p, vr[it].y, o[1]);
+      o[2] = fmaf(p, vr[it].z, o[2]);
+      o[3] = fmaf(p, vr[it].w, o[3]);
+    }
+  }
+  // merge (m, l, o) of (m2, l2, o2) into this lane's triple
+  auto merge = [&](float m2, float l2, const float* o2) {
+    const float m_new = fmaxf(m_run, m2);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float a1 = __builtin_amdgcn_exp2f(m_run - m_use);
+    const float a2 = __builtin_amdgcn_exp2f(m2 - m_use);
+    m_run = m_new;
+    l = l * a1 + l2 * a2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = o[e] * a1 + o2[e] * a2;
+  };
+#pragma unroll
+  for (int off = LPK; off < 64; off <<= 1) {
+    const float m2 = __shfl_xor(m_run, off, 64), l2 = __shfl_xor(l, off, 64);
+    float o2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o2[e] = __shfl_xor(o[e], off, 64);
+    merge(m2, l2, o2);
+  }
+  if (lane < LPK) {
+    *reinterpret_cast<float4*>(&s_o[wave][d4]) = make_float4(o[0], o[1], o[2], o[3]);
+    if (lane == 0) {
+      s_m[wave] = m_run;
+      s_l[wave] = l;
+    }
+  }
+  __syncthreads();
+  if (wave == 0 && lane < LPK) {
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) {
+      const float4 t = *reinterpret_cast<const float4*>(&s_o[w][d4]);
+      const float o2[4] = {t.x, t.y, t.z, t.w};
+      merge(s_m[w], s_l[w], o2);
+    }
+    // no allowed key: 0 / 0, as the blocked kernels give
+    *reinterpret_cast<float4*>(out + (b * sh.q_bstride + qi) * sh.ldo + int64_t(h) * DH + d4) =
+        make_float4(o[0] / l, o[1] / l, o[2] / l, o[3] / l);
+  }
+}
+
+constexpr int kDecodeMaxQ = 8;  // queries per step taken by the decode kernel
+
+template <int DH>
+void launch_attention_decode(const float* q, const float* k, const float* v, const AttnShape& sh,
+                             float* out) {
+  const dim3 grid(unsigned(sh.seq_q), unsigned(sh.heads), unsigned(sh.batch));
+  attention_decode_kernel<DH, 16, 12><<<grid, 1024, 0, stream()>>>(q, k, v, sh, out);
+}
+
 void attention(const float* q, const float* k, const float* v, const AttnShape& sh, int head_dim,
                float* out) {
+  if (sh.seq_q <= kDecodeMaxQ) {
+    switch (head_dim) {
+      case 16: launch_attention_decode<16>(q, k, v, sh, out); break;
+      case 32: launch_attention_decode<32>(q, k, v, sh, out); break;
+      case 64: launch_attention_decode<64>(q, k, v, sh, out); break;
+      case 128: launch_attention_decode<128>(q, k, v, sh, out); break;
+      default:
+        fail(ENQ_ERR_UNSUPPORTED, "attention head_dim %d is not one of 16, 32, 64, 128",
+             head_dim);
+    }
+    check_launch("attention_decode_kernel");
+    return;
+  }
   const dim3 grid(unsigned(ceil_div(sh.seq_q, kAttnQ)), unsigned(sh.heads), unsigned(sh.batch));
   switch (head_dim) {
     case 16:

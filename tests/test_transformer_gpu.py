@@ -110,6 +110,11 @@ KV_CASES = [
     (1, 5, 129, 2, 1, 32, False, None),
     (3, 70, 140, 2, 2, 64, True, None),
     (2, 1, 90, 2, 2, 16, True, 10),
+    # up to 8 queries take the decode kernel: a long cache under a window, a
+    # window of 0 (one key per query), and 9 queries on the blocked kernel
+    (2, 1, 3000, 8, 2, 64, True, 1000),
+    (1, 8, 700, 4, 1, 128, False, 0),
+    (2, 9, 100, 2, 2, 32, True, None),
 ]
 
 
