@@ -354,7 +354,8 @@ int enq_add(const float* a, const float* b, int64_t n, float* y);
  * occupies columns [h*D, (h+1)*D); a fused QKV projection output is passed
  * as three pointers into one buffer with the same row stride.  head_dim is
  * 16, 32, 64 or 128 (other values: ENQ_ERR_UNSUPPORTED); rows 16-byte
- * aligned.  Products are fp32-accurate: at head_dim 32-128 each is six bf16
+ * aligned.  Products are fp32-accurate: with at most 8 queries per sequence
+ * they are fp32 FMAs; otherwise at head_dim 32-128 each is six bf16
  * matrix-core products of the operands' three-part bf16 splits (within about
  * 2^-25 of the fp32 product), at 16 an fp32 matrix-core product; sums and
  * exponentials are fp32. */
