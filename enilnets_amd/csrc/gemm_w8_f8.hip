@@ -798,3 +798,55 @@ extern "C" int enq_gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const in
     finish_rows(y, m, n, ep, false);
   });
 }
+
+extern "C" int enq_dense_w8_ffn(const float* x, int64_t m, int64_t k, const int8_t* codes1,
+                                const float* scale1, int64_t n1, const float* bias1, int act1,
+                                float alpha1, float clip1, const int8_t* codes2,
+                                const float* scale2, int64_t n2, const float* bias2, int act2,
+                                float alpha2, float clip2, int variant, float* y) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(m >= 1 && k >= 1 && n1 >= 1 && n2 >= 1,
+                "m, k, n1, n2 must be positive (m=%lld k=%lld n1=%lld n2=%lld)", (long long)m,
+                (long long)k, (long long)n1, (long long)n2);
+    ENQ_REQUIRE(x && codes1 && scale1 && codes2 && scale2 && y, "NULL pointer argument");
+    ENQ_REQUIRE(valid_activation(act1) && valid_activation(act2), "unknown activation code");
+    ENQ_REQUIRE(variant == ENQ_W8_FP32 || variant == ENQ_W8_BF16, "unknown variant %d", variant);
+    const Epilogue ep1{act1, alpha1, clip1}, ep2{act2, alpha2, clip2};
+    // the split path where enq_dense_w8 takes it for both layers (more than
+    // 2^33 multiply-adds or a full round of 256 x 256 tiles each)
+    const auto split_size = [&](int64_t n, int64_t kk) {
+      return ceil_div(m, 256) * ceil_div(n, 256) >= device_cu_count() ||
+             double(m) * double(n) * double(kk) > 8589934592.0;
+    };
+    const bool fused = variant == ENQ_W8_FP32 && m > 64 && f16f8_supported(k, codes1) &&
+                       f16f8_supported(n1, codes2) && n1 % kF8KPad == 0 &&
+                       act1 != ENQ_ACT_SOFTMAX && split_size(n1, k) && split_size(n2, n1);
+    if (!fused) {
+      // two Dense calls through an fp32 hidden buffer (their own workspace
+      // is the kernel slot, the hidden rows the layer slot)
+      auto* h = static_cast<float*>(workspace(size_t(m) * size_t(n1) * sizeof(float), kLayerSlot));
+      dense_w8(x, m, k, codes1, scale1, n1, bias1, ep1, variant, h, nullptr);
+      dense_w8(h, m, n1, codes2, scale2, n2, bias2, ep2, variant, y, nullptr);
+      return;
+    }
+    // x split once with the hidden rows' exponents (from the bound on the
+    // first layer's outputs); the first GEMM writes the activated hidden
+    // rows straight as the second GEMM's split
+    const size_t b1 = ceil_div(int64_t(f16f8_bytes(m, k)), 256) * 256;
+    const size_t b2 = ceil_div(int64_t(f16f8_bytes(m, n1)), 256) * 256;
+    char* ws = static_cast<char*>(
+        workspace(b1 + b2 + sizeof(float) * (2 + kBoundParts), kLayerSlot));
+    char* split1 = ws;
+    char* split2 = ws + b1;
+    auto* bound = reinterpret_cast<float*>(ws + b1 + b2);
+    int* exps2 = reinterpret_cast<int*>(split2 + 3 * m * f16f8_k_pad(n1));
+    f16f8_bound_params(codes1, n1, k, scale1, bias1, ep1, bound);
+    split_f16f8(x, m, k, split1, nullptr, bound, exps2);
+    gemm_w8_f16f8_grouped(split1, m, k, codes1, scale1, n1, bias1, RowGroups{}, ep1, nullptr,
+                          split2);
+    gemm_w8_f16f8(split2, m, n1, codes2, scale2, n2, bias2, gemm_epilogue(ep2, false), y,
+                  nullptr);
+    finish_rows(y, m, n2, ep2, false);
+  });
+}

@@ -121,6 +121,32 @@ def dense_w8(x: DeviceArray, w: Int8Weights, bias: Optional[DeviceArray] = None,
     return y
 
 
+def dense_w8_ffn(x: DeviceArray, w1: Int8Weights, b1: Optional[DeviceArray], act1: str,
+                 w2: Int8Weights, b2: Optional[DeviceArray] = None, act2: str = "linear",
+                 variant: str = "fp32", out: Optional[DeviceArray] = None,
+                 params1: Optional[Dict[str, Any]] = None,
+                 params2: Optional[Dict[str, Any]] = None) -> DeviceArray:
+    """Two Dense layers in a row, ``act2(act1(x W1^T + b1) W2^T + b2)``, when
+    only the second output is wanted (a transformer block's feed-forward
+    pair): ``dense_w8`` twice, except that at large sizes the first GEMM
+    writes its output straight as the second's fp16/e4m3 split."""
+    if x.dtype != np.float32:
+        raise NotImplementedError(f"W8 Dense takes float32 activations, got {x.dtype}")
+    m, k = _rows(x)
+    if len(w1.shape) != 2 or len(w2.shape) != 2:
+        raise ValueError("dense weights must be 2-D")
+    n1, n2 = w1.shape[0], w2.shape[0]
+    if w1.shape[1] != k or w2.shape[1] != n1:
+        raise ValueError(f"shapes {x.shape}, {w1.shape} and {w2.shape} not aligned")
+    c1, a1, k1 = activation_args(act1, params1)
+    c2, a2, k2 = activation_args(act2, params2)
+    y = out if out is not None else DeviceArray(x.shape[:-1] + (n2,), np.float32)
+    _lib.call("enq_dense_w8_ffn", x.ptr, m, k, w1.codes.ptr, w1.scale.ptr, n1,
+              b1.ptr if b1 is not None else null(), c1, a1, k1, w2.codes.ptr, w2.scale.ptr, n2,
+              b2.ptr if b2 is not None else null(), c2, a2, k2, VARIANTS[variant], y.ptr)
+    return y
+
+
 class ActivationPlanes:
     """Activations split once into the bf16 planes the tile kernels read
     (``split_planes``), for several ``dense_w8_planes`` calls."""

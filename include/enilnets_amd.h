@@ -252,6 +252,26 @@ int enq_gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes
                       const float* w_scale, int64_t n, const float* bias, int activation,
                       float act_alpha, float act_clip, float* y, float* z);
 
+/* Two Dense layers in a row (a transformer block's feed-forward pair):
+ * y = act2(act1(x . W1^T + b1) . W2^T + b2), W1 = codes1 (n1, k) * scale1,
+ * W2 = codes2 (n2, n1) * scale2, biases nullable, each layer as
+ * enq_dense_w8 with its activation (act1 not softmax on the fused path).
+ * Replaces two consecutive Dense branches of forward.py:318-321 when only
+ * the second output is wanted.  For the fp32-accurate variant at sizes where
+ * enq_dense_w8 takes the fp16/e4m3 split for both layers (k and n1 multiples
+ * of 16, n1 of 64, aligned codes), the first GEMM writes its activated
+ * output straight as the second's split, with row exponents from a bound on
+ * the first layer's outputs (||x_r||_2 times the largest weight row norm,
+ * plus the bias): no fp32 hidden rows in HBM and no split pass over them;
+ * y within 1e-4 * max |z2| per row of the float64 result.  Otherwise two
+ * enq_dense_w8 calls through an fp32 hidden buffer.  No counterpart in the
+ * reference as one call. */
+int enq_dense_w8_ffn(const float* x, int64_t m, int64_t k, const int8_t* codes1,
+                     const float* scale1, int64_t n1, const float* bias1, int act1,
+                     float alpha1, float clip1, const int8_t* codes2, const float* scale2,
+                     int64_t n2, const float* bias2, int act2, float alpha2, float clip2,
+                     int variant, float* y);
+
 /* enq_dense_w8 without any allocation.  No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same

@@ -337,3 +337,34 @@ def test_w8a8_static(gpu, m, k, n, spec_i):
                      x_spec=spec).numpy()
     err = np.max(np.abs(y - np.maximum(z_ref, 0)), axis=1) / np.max(np.abs(z_ref), axis=1)
     assert np.all(err <= 1e-4), f"max row error {err.max():.3e}"
+
+
+# (m, k, n1, n2, act1, bias): the configs[3] feed-forward pair (fused: the
+# first GEMM writes the second's fp16/e4m3 split), a ReLU pair with biases
+# (fused), and a small pair through two Dense calls
+FFN_CASES = [(4096, 1024, 4096, 1024, "gelu", False), (4096, 512, 8192, 1024, "relu", True),
+             (300, 96, 200, 50, "gelu", True)]
+
+
+@pytest.mark.parametrize("m,k,n1,n2,act1,bias", FFN_CASES)
+def test_dense_w8_ffn(gpu, m, k, n1, n2, act1, bias):
+    print(f"[case] dense_w8_ffn m={m} k={k} n1={n1} n2={n2} {act1} bias={bias}", flush=True)
+    x, fq1, _, _, bb1, wq1 = make(m, k, n1, seed=m + k + n1, wstd=0.02)
+    _, fq2, _, _, bb2, wq2 = make(8, n1, n2, seed=n1 + n2, wstd=0.02)
+    if not bias:
+        bb1, bb2 = np.zeros_like(bb1), np.zeros_like(bb2)
+    d_x = DeviceArray.from_numpy(x)
+    d_b1, d_b2 = DeviceArray.from_numpy(bb1), DeviceArray.from_numpy(bb2)
+    y = D.dense_w8_ffn(d_x, wq1, d_b1, act1, wq2, d_b2, "linear").numpy()
+    # rows checked against float64 on a sample of at most 64
+    pick = np.unique(np.linspace(0, m - 1, min(m, 64)).astype(np.int64))
+    h = oracle.activate(act1, x[pick].astype(np.float64) @ fq1.astype(np.float64).T + bb1)
+    ref = h @ fq2.astype(np.float64).T + bb2
+    err = row_rel_err(y[pick].astype(np.float64), ref)
+    assert np.all(err <= 1e-4), f"max row error {err.max():.3e}"
+    assert np.isfinite(y).all()
+    # the same as two dense_w8 calls, to the same bar
+    h2 = D.dense_w8(d_x, wq1, d_b1, act1)
+    y2 = D.dense_w8(h2, wq2, d_b2, "linear").numpy()
+    assert np.all(row_rel_err(y2[pick].astype(np.float64), ref) <= 1e-4)
+    assert np.all(row_rel_err(y.astype(np.float64), y2.astype(np.float64)) <= 2e-4)
