@@ -563,7 +563,7 @@ def transformer_block(timer, rng):
     from enilnets_amd.device import DeviceArray
     from enilnets_amd.nn import Model, int8_weights
     from enilnets_amd.nn import transformer as T
-    from enilnets_amd.nn.dense import dense_w8_ffn
+    from enilnets_amd.nn.dense import dense_w8_ffn, ffn_bound
     B, S, E, F, H = 8, 512, 1024, 4096, 16
     m = Model()
     m.add_residual_start()
@@ -585,14 +585,16 @@ def transformer_block(timer, rng):
     w1, w2 = int8_weights(L[6], "weights"), int8_weights(L[7], "weights")
     b1, b2 = DeviceArray.from_numpy(L[6]["bias"]), DeviceArray.from_numpy(L[7]["bias"])
     t1, a1, r1, t2, f2, y = (DeviceArray((B, S, E), np.float32) for _ in range(6))
+    fb = ffn_bound(w1, b1, "gelu")
 
     def block(_=0):
         T.layernorm(x, L[1], out=t1, params=ln1)
         T.mha_forward(t1, L[2], plan=plan, out=a1)
         T.residual_add(a1, x, out=r1)
         T.layernorm(r1, L[5], out=t2, params=ln2)
-        # the FFN pair: the first GEMM writes the second's fp16/e4m3 split
-        dense_w8_ffn(t2, w1, b1, "gelu", w2, b2, "linear", out=f2)
+        # the FFN pair: the first GEMM writes the second's fp16/e4m3 split,
+        # with FFN1's output bound computed once, as the weights are quantized
+        dense_w8_ffn(t2, w1, b1, "gelu", w2, b2, "linear", out=f2, bound=fb)
         T.residual_add(f2, r1, out=y)
 
     block()

@@ -95,8 +95,9 @@ SIGNATURES = {
     "enq_gemm_w8_f16f8": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, _P, c_int, c_float,
                                   c_float, _P, _P]),
     "enq_dense_w8_ffn": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, _P, c_int, c_float,
-                                 c_float, _P, _P, c_int64, _P, c_int, c_float, c_float, c_int,
-                                 _P]),
+                                 c_float, _P, _P, _P, c_int64, _P, c_int, c_float, c_float,
+                                 c_int, _P]),
+    "enq_f16f8_bound": (c_int, [_P, c_int64, c_int64, _P, _P, c_int, c_float, c_float, _P]),
     "enq_dense_w8_noalloc": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, _P, c_int, c_float,
                                      c_float, c_int, _P, _P]),
     "enq_gemm_w8a8": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int, c_float,

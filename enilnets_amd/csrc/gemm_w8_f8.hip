@@ -707,6 +707,11 @@ void split_f16f8(const float* x, int64_t m, int64_t k, void* buf, const int* gat
 
 void f16f8_bound_params(const int8_t* codes, int64_t rows, int64_t k, const float* w_scale,
                         const float* bias, const Epilogue& ep, float* out) {
+  f16f8_bound_params(codes, rows, k, w_scale, bias, ep, out, out + 2);
+}
+
+void f16f8_bound_params(const int8_t* codes, int64_t rows, int64_t k, const float* w_scale,
+                        const float* bias, const Epilogue& ep, float* out, float* part) {
   ENQ_REQUIRE(f16f8_supported(k, codes), "code norms need K a multiple of 16 and aligned codes");
   float c = 1.0f, d = 0.0f;
   switch (ep.activation) {
@@ -717,7 +722,6 @@ void f16f8_bound_params(const int8_t* codes, int64_t rows, int64_t k, const floa
     case ENQ_ACT_SOFTPLUS: d = 0.7f; break;
     default: break;
   }
-  float* part = out + 2;
   const int parts = int(std::min<int64_t>(kBoundParts, ceil_div(rows, 4)));
   code_norm_kernel<<<unsigned(parts), 256, 0, stream()>>>(codes, rows, k, w_scale, part);
   check_launch("code_norm_kernel");
@@ -801,9 +805,10 @@ extern "C" int enq_gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const in
 
 extern "C" int enq_dense_w8_ffn(const float* x, int64_t m, int64_t k, const int8_t* codes1,
                                 const float* scale1, int64_t n1, const float* bias1, int act1,
-                                float alpha1, float clip1, const int8_t* codes2,
-                                const float* scale2, int64_t n2, const float* bias2, int act2,
-                                float alpha2, float clip2, int variant, float* y) {
+                                float alpha1, float clip1, const float* bound1,
+                                const int8_t* codes2, const float* scale2, int64_t n2,
+                                const float* bias2, int act2, float alpha2, float clip2,
+                                int variant, float* y) {
   return guarded([&] {
     require_init();
     ENQ_REQUIRE(m >= 1 && k >= 1 && n1 >= 1 && n2 >= 1,
@@ -836,17 +841,35 @@ extern "C" int enq_dense_w8_ffn(const float* x, int64_t m, int64_t k, const int8
     const size_t b1 = ceil_div(int64_t(f16f8_bytes(m, k)), 256) * 256;
     const size_t b2 = ceil_div(int64_t(f16f8_bytes(m, n1)), 256) * 256;
     char* ws = static_cast<char*>(
-        workspace(b1 + b2 + sizeof(float) * (2 + kBoundParts), kLayerSlot));
+        workspace(b1 + b2 + (bound1 ? 0 : sizeof(float) * (2 + kBoundParts)), kLayerSlot));
     char* split1 = ws;
     char* split2 = ws + b1;
-    auto* bound = reinterpret_cast<float*>(ws + b1 + b2);
     int* exps2 = reinterpret_cast<int*>(split2 + 3 * m * f16f8_k_pad(n1));
-    f16f8_bound_params(codes1, n1, k, scale1, bias1, ep1, bound);
+    const float* bound = bound1;
+    if (!bound) {
+      auto* b = reinterpret_cast<float*>(ws + b1 + b2);
+      f16f8_bound_params(codes1, n1, k, scale1, bias1, ep1, b);
+      bound = b;
+    }
     split_f16f8(x, m, k, split1, nullptr, bound, exps2);
     gemm_w8_f16f8_grouped(split1, m, k, codes1, scale1, n1, bias1, RowGroups{}, ep1, nullptr,
                           split2);
     gemm_w8_f16f8(split2, m, n1, codes2, scale2, n2, bias2, gemm_epilogue(ep2, false), y,
                   nullptr);
     finish_rows(y, m, n2, ep2, false);
+  });
+}
+
+extern "C" int enq_f16f8_bound(const int8_t* codes, int64_t rows, int64_t k, const float* scale,
+                               const float* bias, int activation, float alpha, float clip,
+                               float* out) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(rows >= 1 && k >= 1, "rows and k must be positive");
+    ENQ_REQUIRE(codes && scale && out, "NULL pointer argument");
+    ENQ_REQUIRE(valid_activation(activation) && activation != ENQ_ACT_SOFTMAX,
+                "activation code %d has no output bound", activation);
+    auto* part = static_cast<float*>(workspace(sizeof(float) * kBoundParts));
+    f16f8_bound_params(codes, rows, k, scale, bias, Epilogue{activation, alpha, clip}, out, part);
   });
 }

@@ -44,6 +44,9 @@ void split_f16f8(const float* x, int64_t m, int64_t k, void* buf, const int* gat
 constexpr int kBoundParts = 1024;
 void f16f8_bound_params(const int8_t* codes, int64_t rows, int64_t k, const float* w_scale,
                         const float* bias, const Epilogue& ep, float* out);
+// The same with the kBoundParts scratch floats at `part` instead of out + 2.
+void f16f8_bound_params(const int8_t* codes, int64_t rows, int64_t k, const float* w_scale,
+                        const float* bias, const Epilogue& ep, float* out, float* part);
 // Row-grouped GEMM on split activations (256 x 256 tiles); with `out_split`
 // the activated (m, n) output is written as the next GEMM's split (n a
 // multiple of 64) with the exponents already in out_split's exponent array.

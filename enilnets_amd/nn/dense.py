@@ -125,11 +125,14 @@ def dense_w8_ffn(x: DeviceArray, w1: Int8Weights, b1: Optional[DeviceArray], act
                  w2: Int8Weights, b2: Optional[DeviceArray] = None, act2: str = "linear",
                  variant: str = "fp32", out: Optional[DeviceArray] = None,
                  params1: Optional[Dict[str, Any]] = None,
-                 params2: Optional[Dict[str, Any]] = None) -> DeviceArray:
+                 params2: Optional[Dict[str, Any]] = None,
+                 bound: Optional[DeviceArray] = None) -> DeviceArray:
     """Two Dense layers in a row, ``act2(act1(x W1^T + b1) W2^T + b2)``, when
     only the second output is wanted (a transformer block's feed-forward
     pair): ``dense_w8`` twice, except that at large sizes the first GEMM
-    writes its output straight as the second's fp16/e4m3 split."""
+    writes its output straight as the second's fp16/e4m3 split.  ``bound``
+    is ``ffn_bound(w1, b1, act1, params1)``, computed once per weight (None:
+    computed in every call)."""
     if x.dtype != np.float32:
         raise NotImplementedError(f"W8 Dense takes float32 activations, got {x.dtype}")
     m, k = _rows(x)
@@ -142,9 +145,23 @@ def dense_w8_ffn(x: DeviceArray, w1: Int8Weights, b1: Optional[DeviceArray], act
     c2, a2, k2 = activation_args(act2, params2)
     y = out if out is not None else DeviceArray(x.shape[:-1] + (n2,), np.float32)
     _lib.call("enq_dense_w8_ffn", x.ptr, m, k, w1.codes.ptr, w1.scale.ptr, n1,
-              b1.ptr if b1 is not None else null(), c1, a1, k1, w2.codes.ptr, w2.scale.ptr, n2,
+              b1.ptr if b1 is not None else null(), c1, a1, k1,
+              bound.ptr if bound is not None else null(), w2.codes.ptr, w2.scale.ptr, n2,
               b2.ptr if b2 is not None else null(), c2, a2, k2, VARIANTS[variant], y.ptr)
     return y
+
+
+def ffn_bound(w: Int8Weights, bias: Optional[DeviceArray], activation: str,
+              activation_params: Optional[Dict[str, Any]] = None) -> DeviceArray:
+    """The output bound of a Dense layer that ``dense_w8_ffn`` uses for its
+    hidden rows' exponents (two floats on the device): a property of the
+    weights, bias and activation only."""
+    n, k = w.shape[-2], w.shape[-1]
+    code, alpha, clip = activation_args(activation, activation_params)
+    out = DeviceArray((2,), np.float32)
+    _lib.call("enq_f16f8_bound", w.codes.ptr, n, k, w.scale.ptr,
+              bias.ptr if bias is not None else null(), code, alpha, clip, out.ptr)
+    return out
 
 
 class ActivationPlanes:

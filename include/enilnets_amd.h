@@ -263,14 +263,26 @@ int enq_gemm_w8_f16f8(const void* buf, int64_t m, int64_t k, const int8_t* codes
  * output straight as the second's split, with row exponents from a bound on
  * the first layer's outputs (||x_r||_2 times the largest weight row norm,
  * plus the bias): no fp32 hidden rows in HBM and no split pass over them;
- * y within 1e-4 * max |z2| per row of the float64 result.  Otherwise two
- * enq_dense_w8 calls through an fp32 hidden buffer.  No counterpart in the
- * reference as one call. */
+ * y within 1e-4 * max |z2| per row of the float64 result.  bound1
+ * (nullable) is that bound's two floats from enq_f16f8_bound for (codes1,
+ * scale1, bias1, act1), computed once per weight; NULL computes it in the
+ * call (two more launches).  Otherwise two enq_dense_w8 calls through an
+ * fp32 hidden buffer.  No counterpart in the reference as one call. */
 int enq_dense_w8_ffn(const float* x, int64_t m, int64_t k, const int8_t* codes1,
                      const float* scale1, int64_t n1, const float* bias1, int act1,
-                     float alpha1, float clip1, const int8_t* codes2, const float* scale2,
-                     int64_t n2, const float* bias2, int act2, float alpha2, float clip2,
-                     int variant, float* y);
+                     float alpha1, float clip1, const float* bound1, const int8_t* codes2,
+                     const float* scale2, int64_t n2, const float* bias2, int act2,
+                     float alpha2, float clip2, int variant, float* y);
+
+/* The output bound of a Dense layer that enq_dense_w8_ffn uses for the
+ * exponents of its hidden rows: out[0..1] (device) = (c * max_n scale_n *
+ * ||codes_n||_2, c * max |bias| + d), each widened by 1%, with
+ * |act(z)| <= c |z| + d for the activation (not softmax); a row x then has
+ * every output
+ * within ||x||_2 * out[0] + out[1].  A property of the weights only, so a
+ * caller computes it once per weight.  No counterpart in the reference. */
+int enq_f16f8_bound(const int8_t* codes, int64_t rows, int64_t k, const float* scale,
+                    const float* bias, int activation, float alpha, float clip, float* out);
 
 /* enq_dense_w8 without any allocation.  No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph

@@ -368,3 +368,7 @@ def test_dense_w8_ffn(gpu, m, k, n1, n2, act1, bias):
     y2 = D.dense_w8(h2, wq2, d_b2, "linear").numpy()
     assert np.all(row_rel_err(y2[pick].astype(np.float64), ref) <= 1e-4)
     assert np.all(row_rel_err(y.astype(np.float64), y2.astype(np.float64)) <= 2e-4)
+    # a bound computed once per weight gives the same output, bit for bit
+    bound = D.ffn_bound(wq1, d_b1, act1)
+    y3 = D.dense_w8_ffn(d_x, wq1, d_b1, act1, wq2, d_b2, "linear", bound=bound).numpy()
+    assert np.array_equal(y3, y)
