@@ -630,7 +630,7 @@ def moe_layer(timer, rng):
     from enilnets_amd.device import DeviceArray
     from enilnets_amd.nn import Int8Weights
     from enilnets_amd.nn.dense import quantize_weight_rows
-    from enilnets_amd.nn.moe import moe_forward
+    from enilnets_amd.nn.moe import moe_bound, moe_forward
     T_, D, Hd, E_, K_ = 8192, 1024, 4096, 8, 2
     layer = {"type": "moe", "embed_dim": D, "num_experts": E_, "hidden_dim": Hd, "top_k": K_,
              "activation": "gelu"}
@@ -643,12 +643,15 @@ def moe_layer(timer, rng):
     x = DeviceArray.from_numpy(rng.standard_normal((T_, D)).astype(np.float32))
     logits = DeviceArray.from_numpy(rng.standard_normal((T_, E_)).astype(np.float32))
     y = DeviceArray((T_, D), np.float32)
+    # the first expert layer's output bound, computed once with the weights
+    bound = moe_bound(layer, weights[0], None)
     _, info = moe_forward(x, layer, router_logits=logits, want_routing=True, out=y,
                           biases=(None, None, None), aux_loss=False,
-                          weights=(weights[0], weights[1], None))
+                          weights=(weights[0], weights[1], None), bound=bound)
     counts = np.bincount(info["top_idx"].numpy().reshape(-1), minlength=E_)
     f = lambda i: moe_forward(x, layer, router_logits=logits, out=y, biases=(None, None, None),
-                              aux_loss=False, weights=(weights[0], weights[1], None))
+                              aux_loss=False, weights=(weights[0], weights[1], None),
+                              bound=bound)
     ms = timer.time(f, 5)
     flops = 2.0 * T_ * K_ * D * Hd * 2
     return {"moe_t8192_e8_top2_d1024_h4096": {

@@ -123,8 +123,8 @@ SIGNATURES = {
     "enq_copy_rows": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64,
                               c_int64]),
     "enq_moe_w8": (c_int, [_P, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                           c_int64, c_int64, c_int, c_int, c_float, c_float, c_int, _P, _P, _P,
-                           _P]),
+                           c_int64, c_int64, c_int, c_int, c_float, c_float, _P, c_int, _P, _P,
+                           _P, _P]),
 }
 
 _lock = threading.RLock()

@@ -367,6 +367,7 @@ struct MoeArgs {
   float* probs;
   int32_t* top_idx;
   double* aux_loss;
+  const float* bound1;  // the first layer's output bound (enq_f16f8_bound), or null
 };
 
 void moe_w8(const MoeArgs& a) {
@@ -451,8 +452,12 @@ void moe_w8(const MoeArgs& a) {
       RowGroups g2{offsets, E, a.d * a.hidden, a.d};
       // the second split's exponents sit after its two planes
       int* exps2 = reinterpret_cast<int*>(split2 + 3 * entries * f16f8_k_pad(a.hidden));
-      f16f8_bound_params(a.w1, E * a.hidden, a.d, a.s1, a.b1, a.ep, bound);
-      split_f16f8(a.x, entries, a.d, split1, row_token, bound, exps2);
+      const float* bnd = a.bound1;
+      if (!bnd) {
+        f16f8_bound_params(a.w1, E * a.hidden, a.d, a.s1, a.b1, a.ep, bound);
+        bnd = bound;
+      }
+      split_f16f8(a.x, entries, a.d, split1, row_token, bnd, exps2);
       gemm_w8_f16f8_grouped(split1, entries, a.d, a.w1, a.s1, a.hidden, a.b1, g1, a.ep, nullptr,
                             split2);
       // K of the second GEMM in two parts, added in the combine: its tiles
@@ -530,8 +535,9 @@ extern "C" int enq_moe_w8(const float* x, int64_t tokens, int64_t d, const float
                           const int8_t* wr, const float* sr, const float* br, const int8_t* w1,
                           const float* s1, const float* b1, const int8_t* w2, const float* s2,
                           const float* b2, int64_t experts, int64_t hidden, int top_k,
-                          int activation, float act_alpha, float act_clip, int variant,
-                          float* out, float* probs, int32_t* top_idx, double* aux_loss) {
+                          int activation, float act_alpha, float act_clip,
+                          const float* bound1, int variant, float* out, float* probs,
+                          int32_t* top_idx, double* aux_loss) {
   return guarded([&] {
     require_init();
     ENQ_REQUIRE(tokens >= 1 && d >= 1 && hidden >= 1,
@@ -551,7 +557,7 @@ extern "C" int enq_moe_w8(const float* x, int64_t tokens, int64_t d, const float
     ENQ_REQUIRE(variant == ENQ_W8_FP32 || variant == ENQ_W8_BF16, "unknown variant %d", variant);
     MoeArgs a{x,  tokens, d,  router_logits, wr, sr, br, w1, s1, b1, w2, s2, b2, experts, hidden,
               top_k, Epilogue{activation, act_alpha, act_clip}, variant, out, probs, top_idx,
-              aux_loss};
+              aux_loss, bound1};
     moe_w8(a);
   });
 }

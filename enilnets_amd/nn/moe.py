@@ -43,7 +43,8 @@ def moe_forward(x: DeviceArray, layer: Dict[str, Any], variant: str = "fp32",
                 want_routing: bool = False, out: Optional[DeviceArray] = None,
                 biases: Optional[Tuple[Optional[DeviceArray], ...]] = None,
                 aux_loss: bool = True,
-                weights: Optional[Tuple[Int8Weights, Int8Weights, Optional[Int8Weights]]] = None
+                weights: Optional[Tuple[Int8Weights, Int8Weights, Optional[Int8Weights]]] = None,
+                bound: Optional[DeviceArray] = None
                 ) -> Tuple[DeviceArray, Dict[str, Any]]:
     """``(out, info)`` for a ``(..., E)`` float32 device array.  ``info``
     holds ``aux_loss`` (a Python float, unless ``aux_loss`` is False) and,
@@ -52,7 +53,8 @@ def moe_forward(x: DeviceArray, layer: Dict[str, Any], variant: str = "fp32",
     benchmark configuration draws the logits directly); ``biases`` passes
     ``moe_biases(layer)`` made once and ``weights`` the ``(W1, W2, Wr)``
     int8 weights, skipping the per-call staleness check of the layer's
-    cache (which hashes the host arrays)."""
+    cache (which hashes the host arrays); ``bound`` passes ``moe_bound`` of
+    those weights, computed once."""
     if x.dtype != np.float32:
         raise NotImplementedError(f"the MoE layer takes float32 activations, got {x.dtype}")
     if layer["activation"] == "softmax":
@@ -93,7 +95,7 @@ def moe_forward(x: DeviceArray, layer: Dict[str, Any], variant: str = "fp32",
     _lib.call("enq_moe_w8", x.ptr, tokens, d, *router, w1.codes.ptr, w1.scale.ptr,
               b1.ptr if b1 is not None else null(), w2.codes.ptr, w2.scale.ptr,
               b2.ptr if b2 is not None else null(), n_exp, hidden, k, code, alpha, clip,
-              VARIANTS[variant], out.ptr, probs.ptr if probs is not None else null(),
+              bound.ptr if bound is not None else null(), VARIANTS[variant], out.ptr, probs.ptr if probs is not None else null(),
               top_idx.ptr if top_idx is not None else null(),
               loss.ptr if loss is not None else null())
     info: Dict[str, Any] = {}
@@ -103,3 +105,18 @@ def moe_forward(x: DeviceArray, layer: Dict[str, Any], variant: str = "fp32",
         info["probs"] = probs
         info["top_idx"] = top_idx
     return out, info
+
+
+def moe_bound(layer: Dict[str, Any], w1: Int8Weights,
+              b1: Optional[DeviceArray]) -> DeviceArray:
+    """The first expert layer's output bound (two floats on the device) that
+    the fp16/e4m3 path of ``moe_forward`` uses for the hidden rows'
+    exponents: ``enq_f16f8_bound`` over the stacked (experts * hidden, d)
+    codes, scales and biases under the layer's activation.  A property of
+    the weights only."""
+    rows, k = w1.shape[0] * w1.shape[1], w1.shape[2]
+    code, alpha, clip = activation_args(layer["activation"], layer.get("activation_params"))
+    out = DeviceArray((2,), np.float32)
+    _lib.call("enq_f16f8_bound", w1.codes.ptr, rows, k, w1.scale.ptr,
+              b1.ptr if b1 is not None else null(), code, alpha, clip, out.ptr)
+    return out

@@ -433,13 +433,17 @@ int enq_copy_rows(const float* src, int64_t ld_src, int64_t src_bstride,
  * be NULL.  Optional outputs: probs (tokens, experts), top_idx (tokens,
  * top_k) int32 in slot order, aux_loss (one double on the device: the
  * load-balancing loss of moe.py:38-49).  experts <= 256; softmax is not an
- * accepted expert activation.  variant as in enq_dense_w8. */
+ * accepted expert activation.  variant as in enq_dense_w8.  bound1
+ * (nullable): enq_f16f8_bound of the stacked first layer (w1 as experts *
+ * hidden rows of d, s1, b1, the activation), computed once per weight; NULL
+ * computes it in the call. */
 int enq_moe_w8(const float* x, int64_t tokens, int64_t d, const float* router_logits,
                const int8_t* wr, const float* sr, const float* br,
                const int8_t* w1, const float* s1, const float* b1,
                const int8_t* w2, const float* s2, const float* b2,
                int64_t experts, int64_t hidden, int top_k,
-               int activation, float act_alpha, float act_clip, int variant,
+               int activation, float act_alpha, float act_clip,
+               const float* bound1, int variant,
                float* out, float* probs, int32_t* top_idx, double* aux_loss);
 
 #ifdef __cplusplus
