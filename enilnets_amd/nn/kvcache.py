@@ -28,7 +28,8 @@ from ..device import DeviceArray, null
 from .dense import dense_w8
 from .forward import _FLOAT64_ACTIVATIONS, _bias
 from .moe import moe_forward
-from .transformer import MhaPlan, _at, _check_supported, embedding, layernorm, positional_encoding
+from .transformer import (MhaPlan, _at, _check_supported, embedding, layernorm, layernorm_params,
+                          positional_encoding)
 from .weights import int8_weights
 
 
@@ -76,10 +77,11 @@ class KVCache:
 
     ``trust_weights`` (not in the reference) is a promise that the model's
     weight and bias arrays are not modified in place during the session:
-    each step then reuses the layers' device weights, biases and attention
-    buffers instead of re-validating the int8 weights against the host
-    arrays (a full hash of every weight per step) and uploading the biases
-    again.  Arrays replaced by new objects are still picked up."""
+    each step then reuses the layers' device weights, biases, LayerNorm
+    parameters and attention buffers instead of re-validating the int8
+    weights against the host arrays (a full hash of every weight per step)
+    and uploading the biases and LayerNorm parameters again.  Arrays
+    replaced by new objects are still picked up."""
 
     def __init__(self, trust_weights: bool = False) -> None:
         self.kv: Dict[int, _KV] = {}
@@ -201,7 +203,11 @@ def cached_forward_step(model: Any, inputs: Any, cache: KVCache, advance_positio
         elif t == "positional_encoding":
             x = positional_encoding(x, layer, pos)
         elif t == "layernorm":
-            x = layernorm(x, layer)
+            # gamma and beta uploaded once per trusted session (each upload
+            # is a synchronous copy that waits for the queued kernels)
+            params = _resources(cache, ("layernorm", idx), layer,
+                                lambda layer=layer: layernorm_params(layer))
+            x = layernorm(x, layer, params=params)
             dtype = np.result_type(dtype, np.asarray(layer["gamma"]).dtype,
                                    np.asarray(layer["beta"]).dtype)
         elif t == "dense":
