@@ -7,6 +7,7 @@ release them per call.
 """
 
 import ctypes
+import math
 from typing import Sequence, Tuple
 
 import numpy as np
@@ -22,7 +23,7 @@ class DeviceArray:
     def __init__(self, shape: Sequence[int], dtype, ptr: int = None, owner=None):
         self.shape: Tuple[int, ...] = tuple(int(s) for s in shape)
         self.dtype = np.dtype(dtype)
-        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        self.nbytes = math.prod(self.shape) * self.dtype.itemsize
         self._owner = owner
         if ptr is None:
             p = ctypes.c_void_p()
@@ -56,7 +57,7 @@ class DeviceArray:
 
     @property
     def size(self) -> int:
-        return int(np.prod(self.shape, dtype=np.int64))
+        return math.prod(self.shape)
 
     @property
     def ndim(self) -> int:
