@@ -278,9 +278,10 @@ int enq_dense_w8_ffn(const float* x, int64_t m, int64_t k, const int8_t* codes1,
  * exponents of its hidden rows: out[0..1] (device) = (c * max_n scale_n *
  * ||codes_n||_2, c * max |bias| + d), each widened by 1%, with
  * |act(z)| <= c |z| + d for the activation (not softmax); a row x then has
- * every output
- * within ||x||_2 * out[0] + out[1].  A property of the weights only, so a
- * caller computes it once per weight.  No counterpart in the reference. */
+ * every output within ||x||_2 * out[0] + out[1].  k a multiple of 16 and
+ * codes 16-byte aligned, as the split GEMM needs.  A property of the
+ * weights only, so a caller computes it once per weight.  No counterpart in
+ * the reference. */
 int enq_f16f8_bound(const int8_t* codes, int64_t rows, int64_t k, const float* scale,
                     const float* bias, int activation, float alpha, float clip, float* out);
 
