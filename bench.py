@@ -600,9 +600,31 @@ def transformer_block(timer, rng):
     block()
     ms = timer.time(block, 10)
     flops = 2.0 * B * S * (3 * E * E + E * E + E * F + F * E)
+    # the same block captured once as a HIP graph and replayed (one launch
+    # instead of a host dispatch per kernel); each checked replay first
+    # clears the output and must give the eager output bit for bit
+    import ctypes
+    from enilnets_amd.graph import capture
+    want = y.numpy()
+    zeros = np.zeros(want.shape, np.float32)
+    graph = capture(block)
+    try:
+        for _ in range(3):
+            _lib.call("enq_copy_to_device", y.ptr, zeros.ctypes.data_as(ctypes.c_void_p),
+                      ctypes.c_size_t(zeros.nbytes))
+            graph.replay()
+            if not np.array_equal(y.numpy(), want):
+                raise RuntimeError("graph replay of the transformer block differs from eager")
+            block()
+        ms_graph = timer.time(lambda i: graph.replay(), 10)
+    finally:
+        graph.close()
     res = {"transformer_block_b8_s512_e1024": {
         "ms": ms, "TFLOP/s": flops / ms / 1e9, "frac_bf16_peak": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
-        "weight_gflop": flops / 1e9, "variant": "fp32"}}
+        "weight_gflop": flops / 1e9, "variant": "fp32",
+        "ms_graph_replay": ms_graph, "TFLOP/s_graph_replay": flops / ms_graph / 1e9,
+        "note": "ms: eager calls from Python; ms_graph_replay: the same calls captured once "
+                "(enq_graph_*) and replayed"}}
     n_all = plan.wqkv.shape[0]
 
     def core(_=0):

@@ -62,6 +62,10 @@ SIGNATURES = {
     "enq_last_error": (c_char_p, []),
     "enq_get_stream": (c_int, [POINTER(c_void_p)]),
     "enq_set_stream": (c_int, [_P]),
+    "enq_graph_begin": (c_int, []),
+    "enq_graph_end": (c_int, [_P]),
+    "enq_graph_launch": (c_int, [_P]),
+    "enq_graph_destroy": (c_int, [_P]),
     "enq_malloc": (c_int, [POINTER(c_void_p), c_size_t]),
     "enq_free": (c_int, [_P]),
     "enq_release_cached_memory": (c_int, []),

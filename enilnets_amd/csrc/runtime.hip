@@ -25,6 +25,9 @@ struct DeviceState {
 
 DeviceState g_state;
 std::mutex g_mutex;
+// captured graphs alive (enq_graph_end .. enq_graph_destroy): their kernels
+// hold workspace addresses, so the workspace may not move meanwhile
+int g_live_graphs = 0;
 
 // The allocation-free entry point's scratch.  Host code never uses this name
 // as an address (on the host it is only a stand-in for the symbol): enq_init
@@ -112,6 +115,11 @@ void* workspace(size_t bytes, int slot) {
   std::lock_guard<std::mutex> lock(g_mutex);
   if (slot != kKernelSlot && slot != kLayerSlot) fail(ENQ_ERR_RUNTIME, "bad workspace slot");
   if (bytes <= g_state.workspace_bytes[slot]) return g_state.workspace[slot];
+  if (g_live_graphs > 0)
+    fail(ENQ_ERR_INVALID,
+         "this call needs %zu bytes of workspace, more than the %zu held while a captured "
+         "graph is alive; destroy the graph first, or run this call once before capturing",
+         bytes, g_state.workspace_bytes[slot]);
   // Round up so repeated small growth does not reallocate every call.
   size_t want = 1u << 20;
   while (want < bytes) want <<= 1;
@@ -236,6 +244,51 @@ int enq_set_stream(void* s) {
     // cached blocks were last used on the old stream
     ENQ_HIP(hipStreamSynchronize(stream()));
     g_state.user_stream = static_cast<hipStream_t>(s);
+  });
+}
+
+int enq_graph_begin(void) {
+  return guarded([&] {
+    require_init();
+    ENQ_HIP(hipStreamBeginCapture(stream(), hipStreamCaptureModeGlobal));
+  });
+}
+
+int enq_graph_end(void** graph) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(graph != nullptr, "graph out-pointer is NULL");
+    *graph = nullptr;
+    hipGraph_t g = nullptr;
+    // ends the capture even when a captured call failed (then with an error)
+    ENQ_HIP(hipStreamEndCapture(stream(), &g));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t err = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    ENQ_HIP(hipGraphDestroy(g));
+    ENQ_HIP(err);
+    std::lock_guard<std::mutex> lock(g_mutex);
+    ++g_live_graphs;
+    *graph = exec;
+  });
+}
+
+int enq_graph_launch(void* graph) {
+  return guarded([&] {
+    require_init();
+    ENQ_REQUIRE(graph != nullptr, "graph is NULL");
+    ENQ_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(graph), stream()));
+  });
+}
+
+int enq_graph_destroy(void* graph) {
+  return guarded([&] {
+    require_init();
+    if (graph == nullptr) return;
+    // replays still queued read the graph's buffers and code
+    ENQ_HIP(hipStreamSynchronize(stream()));
+    ENQ_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph)));
+    std::lock_guard<std::mutex> lock(g_mutex);
+    --g_live_graphs;
   });
 }
 

@@ -99,6 +99,21 @@ int enq_get_stream(void** stream);
 /* Launch on a caller-owned stream instead (NULL restores the library's). */
 int enq_set_stream(void* stream);
 
+/* HIP graph of a fixed sequence of calls, for callers that repeat it (a
+ * serving loop's layer): enq_graph_begin starts capturing the library
+ * stream; the calls that follow are recorded, not run; enq_graph_end stops
+ * and instantiates the graph (an error if a recorded call failed or
+ * synchronised); enq_graph_launch replays it on the library stream;
+ * enq_graph_destroy waits for the stream and frees it.  Run every call once
+ * before capturing it: while a graph is alive the library's workspace does
+ * not grow (a call needing more fails with ENQ_ERR_INVALID), and the
+ * buffers the recorded calls use must stay allocated.  No counterpart in
+ * the reference. */
+int enq_graph_begin(void);
+int enq_graph_end(void** graph);
+int enq_graph_launch(void* graph);
+int enq_graph_destroy(void* graph);
+
 /* ---- device memory -------------------------------------------------- */
 /* Device buffers from a caching allocator: enq_free keeps the block for the
  * next enq_malloc of its size class instead of returning it to HIP (work
