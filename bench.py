@@ -191,6 +191,7 @@ def cpu_baseline(x, w, fq, codes, scale):
 def mlp_step(timer, rng, steps, warmup):
     """the three fused dequant-GEMMs of the MLP at batch
     4096 (fp32-accurate W8), inputs resident in HBM."""
+    from enilnets_amd import _lib
     from enilnets_amd.device import DeviceArray
     from enilnets_amd.nn import int8_weights
     from enilnets_amd.nn.dense import dense_w8
@@ -214,6 +215,24 @@ def mlp_step(timer, rng, steps, warmup):
     for _ in range(warmup):
         step()
     ms = timer.time(step, steps)
+    # the same step captured once as a HIP graph and replayed; each checked
+    # replay first clears the output and must give the eager output bit for bit
+    import ctypes
+    from enilnets_amd.graph import capture
+    want = outs[-1].numpy()
+    zeros = np.zeros(want.shape, np.float32)
+    graph = capture(step)
+    try:
+        for _ in range(3):
+            _lib.call("enq_copy_to_device", outs[-1].ptr, zeros.ctypes.data_as(ctypes.c_void_p),
+                      ctypes.c_size_t(zeros.nbytes))
+            graph.replay()
+            if not np.array_equal(outs[-1].numpy(), want):
+                raise RuntimeError("graph replay of the MLP step differs from eager")
+            step()
+        ms_graph = timer.time(lambda i: graph.replay(), steps)
+    finally:
+        graph.close()
     # the largest layer's GEMM (4096 x 1024 x 1024), one kernel, timed alone
     big = int(np.argmax([w.shape[0] * w.shape[1] for w in ws]))
     h_in = d_x if big == 0 else outs[big - 1]
@@ -223,6 +242,7 @@ def mlp_step(timer, rng, steps, warmup):
     return {"mlp_step_config1": {
         "ms": ms, "TFLOP/s": flops / ms / 1e9, "frac_bf16_peak": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
         "gflop": flops / 1e9, "variant": "fp32",
+        "ms_graph_replay": ms_graph, "TFLOP/s_graph_replay": flops / ms_graph / 1e9,
         "largest_layer": {"shape": [M, ws[big].shape[0], ws[big].shape[1]], "ms": k_ms,
                           "TFLOP/s": k_flops / k_ms / 1e9,
                           "frac_bf16_peak": k_flops / k_ms / 1e9 / BF16_PEAK_TFLOPS,
