@@ -372,3 +372,20 @@ def test_dense_w8_ffn(gpu, m, k, n1, n2, act1, bias):
     bound = D.ffn_bound(wq1, d_b1, act1)
     y3 = D.dense_w8_ffn(d_x, wq1, d_b1, act1, wq2, d_b2, "linear", bound=bound).numpy()
     assert np.array_equal(y3, y)
+
+
+def test_dense_w8_ffn_bf16_and_errors(gpu):
+    # the bf16 variant takes two Dense calls (bf16 bar, 2e-2 of the row)
+    x, fq1, _, _, bb1, wq1 = make(512, 256, 512, seed=5, wstd=0.02)
+    _, fq2, _, _, bb2, wq2 = make(8, 512, 128, seed=6, wstd=0.02)
+    d_x = DeviceArray.from_numpy(x)
+    d_b1, d_b2 = DeviceArray.from_numpy(bb1), DeviceArray.from_numpy(bb2)
+    y = D.dense_w8_ffn(d_x, wq1, d_b1, "gelu", wq2, d_b2, "linear", variant="bf16").numpy()
+    h = oracle.activate("gelu", x.astype(np.float64) @ fq1.astype(np.float64).T + bb1)
+    ref = h @ fq2.astype(np.float64).T + bb2
+    assert np.all(row_rel_err(y.astype(np.float64), ref) <= 2e-2)
+    # misaligned shapes, and an output bound for softmax (which has none)
+    with pytest.raises(ValueError):
+        D.dense_w8_ffn(d_x, wq1, d_b1, "gelu", wq1, d_b2, "linear")
+    with pytest.raises(ValueError):
+        D.ffn_bound(wq1, d_b1, "softmax")
